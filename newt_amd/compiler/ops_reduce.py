@@ -1,0 +1,157 @@
+"""nl.sum / nl.max / nl.min lowering.
+
+Semantics (reference newt/compiler/codegen.py:1883-1999): fp16/bf16 reduce to an
+fp32 result, a bool block reduces to an int32 count (sum) or "any" (max);
+identities are 0, -inf/+inf, INT_MIN/INT_MAX; float max/min are fmaxf/fminf.
+
+Lowering (this backend's own): the reduced dimension's logical bits are split
+by the hardware index that carries them in the operand's layout -
+  register bits -> combined in-thread,
+  lane bits     -> wave64 butterfly (newt::lane_reduce: DPP quad_perm for
+                   xor 1/2, ds_swizzle for xor 4..16, ds_bpermute for xor 32),
+  wave bits     -> one LDS exchange + barrier.
+Replicated hardware bits are never combined (they hold copies). The result of
+an axis reduction keeps the operand's layout minus the reduced bits, so a row
+statistic of an MFMA tile stays one-row-per-lane and broadcasts back for free.
+"""
+
+import math
+
+from . import types as tp
+from .values import Block, Const, LazyLoad, Reg, Scalar
+
+_OPS = {"sum": "newt::Sum", "max": "newt::Max", "min": "newt::Min"}
+
+
+class ReduceOps:
+    def _identity(self, op, dt):
+        if op == "sum":
+            return self.literal(0, dt)
+        if dt.is_floating:
+            return self.literal(float("-inf") if op == "max" else float("inf"), dt)
+        if dt == tp.int64:
+            return "(-9223372036854775807LL - 1)" if op == "max" else "9223372036854775807LL"
+        if dt == tp.uint32:
+            return "0u" if op == "max" else "4294967295u"
+        return "(-2147483647 - 1)" if op == "max" else "2147483647"
+
+    def _combine(self, op, a, b):
+        return f"{_OPS[op]}::op({a}, {b})"
+
+    def _reduce(self, node, x, axis, op):
+        if isinstance(x, (Const, Scalar)):
+            return x
+        if isinstance(x, LazyLoad):
+            x = self.materialize_load(x)
+        rt = tp.float32 if tp.is_half(x.dtype) else x.dtype
+        if rt == tp.int1:
+            rt = tp.int32
+        x = self.to_reg(x) if not isinstance(x, Reg) else x
+        if axis is not None:
+            ax = self._cx(node, axis, "axis") if not isinstance(axis, int) else axis
+            if ax < 0:
+                ax += len(x.shape)
+            if ax >= len(x.shape):
+                self.err(node, f"axis {ax} out of range for shape {x.shape}")
+            if len(x.shape) > 1:
+                return self._reduce_axis(x, ax, op, rt)
+        return self._reduce_full(x, op, rt)
+
+    def _lds_for_reduce(self, nbytes):
+        if self.loop_depth:
+            self.barrier()
+        return self.lds_alloc(nbytes)
+
+    def _reduce_full(self, x, op, rt):
+        L = x.layout
+        p = self.fresh("rp")
+        first = True
+        for s in range(L.nslots):
+            if not L.slot_is_canonical(s):
+                continue
+            e = self.conv(x.at(s), x.dtype, rt)
+            if first:
+                self.emit(f"{rt.ctype} {p} = {e};")
+                first = False
+            else:
+                self.emit(f"{p} = {self._combine(op, p, e)};")
+        lmask = sum(1 << i for i, b in enumerate(L.lane) if b is not None)
+        if lmask:
+            self.emit(f"{p} = newt::lane_reduce<{_OPS[op]}, {lmask}>({p});")
+        wbits = [i for i, b in enumerate(L.wave) if b is not None]
+        if wbits:
+            n = 1 << len(wbits)
+            region = self._lds_for_reduce(n * max(rt.itemsize, 4))
+            buf = self.fresh("rb")
+            self.emit(f"{rt.ctype}* {buf} = ({rt.ctype}*)(_lds + {region});")
+            idx = " | ".join(f"(((_wave >> {w}) & 1) << {k})" for k, w in enumerate(wbits))
+            rep = L.wave_rep_mask()
+            cond = "_lane == 0" + (f" && (_wave & {rep}) == 0" if rep else "")
+            self.emit(f"if ({cond}) {buf}[{idx}] = {p};")
+            self.barrier()
+            self.emit(f"{p} = {buf}[0];")
+            for i in range(1, n):
+                self.emit(f"{p} = {self._combine(op, p, f'{buf}[{i}]')};")
+        return Scalar(rt, p)
+
+    def _reduce_axis(self, x, axis, op, rt):
+        L = x.layout
+        Lr = L.reduce(axis)
+        keep = [i for i, b in enumerate(L.reg) if b is None or b[0] != axis]
+        out = self.new_reg(rt, Lr.shape, Lr)
+        seen = set()
+        for s in range(L.nslots):
+            if not L.slot_is_canonical(s):
+                continue  # replicated register copy
+            t = 0
+            for k, i in enumerate(keep):
+                if (s >> i) & 1:
+                    t |= 1 << k
+            e = self.conv(x.at(s), x.dtype, rt)
+            if t not in seen:
+                self.emit(f"{out.at(t)} = {e};")
+                seen.add(t)
+            else:
+                self.emit(f"{out.at(t)} = {self._combine(op, out.at(t), e)};")
+        lmask = sum(1 << i for i, b in enumerate(L.lane) if b is not None and b[0] == axis)
+        if lmask:
+            for t in range(Lr.nslots):
+                if not Lr.slot_is_canonical(t):
+                    continue
+                self.emit(f"{out.at(t)} = newt::lane_reduce<{_OPS[op]}, {lmask}>({out.at(t)});")
+        wbits = [i for i, b in enumerate(L.wave) if b is not None and b[0] == axis]
+        if wbits:
+            n = 1 << len(wbits)
+            numel = math.prod(Lr.shape) if Lr.shape else 1
+            region = self._lds_for_reduce(n * numel * max(rt.itemsize, 4))
+            buf = self.fresh("rb")
+            self.emit(f"{rt.ctype}* {buf} = ({rt.ctype}*)(_lds + {region});")
+            widx = " | ".join(f"(((_wave >> {w}) & 1) << {k})" for k, w in enumerate(wbits))
+            strides = self._strides(Lr.shape)
+            for t in range(Lr.nslots):
+                if not Lr.slot_is_canonical(t):
+                    continue
+                flat = self._flat_index(Lr, t, strides)
+                self.emit(f"{buf}[({widx}) * {numel} + {flat}] = {out.at(t)};")
+            self.barrier()
+            for t in range(Lr.nslots):
+                if not Lr.slot_is_canonical(t):
+                    continue
+                flat = self._flat_index(Lr, t, strides)
+                self.emit(f"{out.at(t)} = {buf}[{flat}];")
+                for i in range(1, n):
+                    self.emit(f"{out.at(t)} = {self._combine(op, out.at(t), f'{buf}[{i * numel} + {flat}]')};")
+        rmask = Lr.reg_rep_mask()
+        for t in range(Lr.nslots):
+            if t & rmask:
+                self.emit(f"{out.at(t)} = {out.at(t & ~rmask)};")
+        return out
+
+    def op_sum(self, node, x, axis=None):
+        return self._reduce(node, x, axis, "sum")
+
+    def op_max(self, node, x, axis=None):
+        return self._reduce(node, x, axis, "max")
+
+    def op_min(self, node, x, axis=None):
+        return self._reduce(node, x, axis, "min")

@@ -1,0 +1,252 @@
+// newt_gfx950.h - hand-written device templates for newt kernels on MI355X (gfx950).
+//
+// Every kernel the newt compiler emits includes this header (hipRTC receives it
+// as an in-memory include). Generated code keeps the per-element arithmetic; the
+// hardware-specific pieces live here:
+//   * 16-byte vector global loads/stores (global_load_dwordx4 / store_dwordx4)
+//   * wave64 cross-lane butterflies on DPP (quad_perm) and ds_swizzle, with a
+//     ds_bpermute fallback only for the xor-32 step across the two wave halves
+//   * MFMA wrappers for the fp16/bf16/fp32 matrix-core instructions of CDNA4
+//   * XOR-swizzled LDS tile addressing for MFMA operand staging
+//   * float atomic max as a CAS loop on vector memory
+// Nothing here writes through the scalar data cache: every store is a vector
+// (global_/ds_) store.
+#pragma once
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef unsigned int u32;
+typedef unsigned long long u64;
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef u32 u32x2 __attribute__((ext_vector_type(2)));
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+
+namespace newt {
+
+// ---------------------------------------------------------------------------
+// Conversions. Round-to-nearest-even both ways, matching torch's casts.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ f16 to_f16(float x) { return (f16)x; }
+__device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
+
+__device__ __forceinline__ float bits_f32(u32 b) { return __builtin_bit_cast(float, b); }
+__device__ __forceinline__ u32 f32_bits(float f) { return __builtin_bit_cast(u32, f); }
+
+// ---------------------------------------------------------------------------
+// Vector memory access: N elements of T as one global transaction of
+// N*sizeof(T) bytes (<= 16). The caller guarantees alignment.
+// ---------------------------------------------------------------------------
+template <int BYTES> struct raw_vec;
+template <> struct raw_vec<1> { typedef unsigned char type; };
+template <> struct raw_vec<2> { typedef unsigned short type; };
+template <> struct raw_vec<4> { typedef u32 type; };
+template <> struct raw_vec<8> { typedef u32x2 type; };
+template <> struct raw_vec<16> { typedef u32x4 type; };
+
+template <typename T, int N>
+struct vec_t {
+  T d[N];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void load_vec(const T* __restrict__ p, T* out) {
+  typedef typename raw_vec<sizeof(T) * N>::type R;
+  R r = *reinterpret_cast<const R*>(p);
+  vec_t<T, N> v = __builtin_bit_cast(vec_t<T, N>, r);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = v.d[i];
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_vec(T* __restrict__ p, const T* in) {
+  typedef typename raw_vec<sizeof(T) * N>::type R;
+  vec_t<T, N> v;
+#pragma unroll
+  for (int i = 0; i < N; ++i) v.d[i] = in[i];
+  *reinterpret_cast<R*>(p) = __builtin_bit_cast(R, v);
+}
+
+__device__ __forceinline__ bool aligned(const void* p, int bytes) {
+  return (reinterpret_cast<u64>(p) & (u64)(bytes - 1)) == 0;
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 butterflies. xor_lane<M>(v) returns v from lane (lane ^ M).
+//   M = 1, 2  : DPP quad_perm (no LDS traffic)
+//   M = 4..16 : ds_swizzle in bitmask mode (and=0x1f, xor=M) inside 32-lane halves
+//   M = 32    : ds_bpermute across the two halves
+// ---------------------------------------------------------------------------
+template <int M>
+__device__ __forceinline__ int xor_lane_i32(int v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "xor mask");
+  if constexpr (M == 1) {
+    return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]
+  } else if constexpr (M < 32) {
+    return __builtin_amdgcn_ds_swizzle(v, 0x1F | (M << 10));
+  } else {
+    int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    return __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, v);
+  }
+}
+
+template <int M, typename T>
+__device__ __forceinline__ T xor_lane(T v) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, xor_lane_i32<M>(__builtin_bit_cast(int, v)));
+  } else if constexpr (sizeof(T) == 8) {
+    u32x2 w = __builtin_bit_cast(u32x2, v);
+    w.x = (u32)xor_lane_i32<M>((int)w.x);
+    w.y = (u32)xor_lane_i32<M>((int)w.y);
+    return __builtin_bit_cast(T, w);
+  } else {
+    int w = (int)v;
+    return (T)xor_lane_i32<M>(w);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ T xor_lane_dyn(T v, int m) {
+  switch (m) {
+    case 1: return xor_lane<1>(v);
+    case 2: return xor_lane<2>(v);
+    case 4: return xor_lane<4>(v);
+    case 8: return xor_lane<8>(v);
+    case 16: return xor_lane<16>(v);
+    default: return xor_lane<32>(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Reduction combiners. Float max/min follow fmaxf/fminf (NaN-ignoring), as the
+// reference's reductions do.
+// ---------------------------------------------------------------------------
+struct Sum {
+  template <typename T> __device__ __forceinline__ static T op(T a, T b) { return a + b; }
+};
+struct Max {
+  __device__ __forceinline__ static float op(float a, float b) { return __builtin_fmaxf(a, b); }
+  __device__ __forceinline__ static double op(double a, double b) { return __builtin_fmax(a, b); }
+  template <typename T> __device__ __forceinline__ static T op(T a, T b) { return a > b ? a : b; }
+};
+struct Min {
+  __device__ __forceinline__ static float op(float a, float b) { return __builtin_fminf(a, b); }
+  __device__ __forceinline__ static double op(double a, double b) { return __builtin_fmin(a, b); }
+  template <typename T> __device__ __forceinline__ static T op(T a, T b) { return a < b ? a : b; }
+};
+
+// Butterfly over the lane bits set in MASK (compile-time), combining with Op.
+template <typename Op, int MASK, typename T>
+__device__ __forceinline__ T lane_reduce(T v) {
+  if constexpr (MASK & 1) v = Op::op(v, xor_lane<1>(v));
+  if constexpr (MASK & 2) v = Op::op(v, xor_lane<2>(v));
+  if constexpr (MASK & 4) v = Op::op(v, xor_lane<4>(v));
+  if constexpr (MASK & 8) v = Op::op(v, xor_lane<8>(v));
+  if constexpr (MASK & 16) v = Op::op(v, xor_lane<16>(v));
+  if constexpr (MASK & 32) v = Op::op(v, xor_lane<32>(v));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Atomics (vector memory). atomic_max on float is a CAS loop.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void atomic_max_f32(float* p, float v) {
+  u32* up = reinterpret_cast<u32*>(p);
+  u32 old = __hip_atomic_load(up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (!(bits_f32(old) >= v)) {
+    u32 assumed = old;
+    old = atomicCAS(up, assumed, f32_bits(v));
+    if (old == assumed) break;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void atomic_add(T* p, T v) { atomicAdd(p, v); }
+template <typename T>
+__device__ __forceinline__ void atomic_max(T* p, T v) { atomicMax(p, v); }
+__device__ __forceinline__ void atomic_max(float* p, float v) { atomic_max_f32(p, v); }
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers (CDNA4). Names spell M x N x K; operands are the per-lane
+// fragments, C is the accumulator fragment. Lane layouts (per instruction, for
+// lane l, A is the MFMA's left operand [M x K], B its right operand [K x N]):
+//   32x32xK (K=16 fp16/bf16, 8 elems/lane): A[l%32][8*(l/32)+e], B[8*(l/32)+e][l%32]
+//   16x16xK (K=32 fp16/bf16, 8 elems/lane): A[l%16][8*(l/16)+e], B[8*(l/16)+e][l%16]
+//   32x32x8 / 16x16x16 (4 elems/lane):      k = 4*(l/32 or l/16) + e
+//   32x32x2 / 16x16x4 f32 (1 elem/lane):    k = l/32 or l/16
+//   C 32x32: C[8*(v/4) + 4*(l/32) + v%4][l%32];  C 16x16: C[4*(l/16) + v][l%16]
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x16 mfma_32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_32x32x8(f16x4 a, f16x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_32x32x8(bf16x4 a, bf16x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                  __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                   __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_32x32x2(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// LDS operand tiles. An MFMA operand tile of ROWS x KD elements of T is stored
+// row-major with the reduction dim contiguous; its 16-byte chunks are XOR
+// swizzled by row so that the per-lane 16-byte fragment reads of consecutive
+// rows spread over all LDS banks (64 banks x 4 B on gfx950: two 128-byte rows
+// fill the banks once, so the swizzle key skips the row's lowest bit).
+// ---------------------------------------------------------------------------
+template <typename T, int KD>
+struct LdsTile {
+  static constexpr int EPC = 16 / (int)sizeof(T);          // elements per chunk
+  static constexpr int CPR = (KD + EPC - 1) / EPC;          // chunks per row
+  static constexpr int ROW_BYTES = CPR * 16;
+  static constexpr int SWZ = CPR >= 8 ? 7 : (CPR >= 4 ? 3 : (CPR >= 2 ? 1 : 0));
+  static constexpr int SHIFT = ROW_BYTES >= 256 ? 0 : (ROW_BYTES == 128 ? 1 : (ROW_BYTES == 64 ? 2 : 3));
+  // element offset of (row r, reduction index k)
+  __device__ __forceinline__ static int off(int r, int k) {
+    int c = k / EPC;
+    int pc = c ^ ((r >> SHIFT) & SWZ);
+    return r * (CPR * EPC) + pc * EPC + (k % EPC);
+  }
+  static constexpr int elems(int rows) { return rows * CPR * EPC; }
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void lds_read(const T* base, int off, T* out) {
+  load_vec<T, N>(base + off, out);
+}
+
+}  // namespace newt

@@ -1,0 +1,282 @@
+"""@newt.jit: compile-on-first-call kernel wrapper for MI355X.
+
+Surface and behaviour follow the reference (newt/runtime/jit.py:72-229):
+arguments bind like a Python call; constexpr parameters are compile-time;
+tensors become pointers (they must be on the current GPU), bools int1, ints
+int32/int64 by range, floats fp32; grids are a tuple, an int, or a callable
+over META (runtime args + constexprs + num_warps); an empty grid is a no-op;
+launches go on torch's current stream and nothing is synchronized.
+
+What differs is the backend: `num_warps` counts wave64s (64 threads each, so at
+most 16); kernels are specialized, as Triton does, on integer arguments equal
+to 1 and on the power-of-two divisibility (up to 16) of integers and of
+pointer addresses; code objects come from hipRTC and are cached on disk under
+~/.newt/cache (NEWT_CACHE_DIR) keyed by the HIP source, the device-template
+header, the target, the hipRTC version and this backend's version; launches pass
+one packed argument buffer through hipModuleLaunchKernel.
+"""
+
+import ast
+import functools
+import hashlib
+import inspect
+import os
+import textwrap
+
+from ..compiler import CompileError, Param, compile_fn
+from ..compiler import types as tp
+from ..compiler.codegen import _CKEYWORDS
+from . import hip as _hip
+
+
+def _cache_dir():
+    d = os.environ.get("NEWT_CACHE_DIR") or os.path.join(os.path.expanduser("~"), ".newt", "cache")
+    os.makedirs(d, exist_ok=True)
+    return d
+
+
+def _is_constexpr_ann(ann):
+    from .. import language as nl
+
+    if ann is nl.constexpr or isinstance(ann, nl.constexpr):
+        return True
+    return isinstance(ann, str) and "constexpr" in ann
+
+
+def _pow2_div(v, cap=16):
+    v = abs(int(v))
+    if v == 0:
+        return cap
+    return min(v & -v, cap)
+
+
+@functools.cache
+def _arch():
+    """gfx target of the current device (the compiler only targets gfx950)."""
+    import torch
+
+    if not torch.cuda.is_available():
+        return _hip.TARGET_ARCH
+    name = _hip.device_arch(torch.cuda.current_device()).split(":")[0]
+    if name != _hip.TARGET_ARCH:
+        raise RuntimeError(f"newt_amd generates code for {_hip.TARGET_ARCH} (MI355X) only; "
+                           f"the current device is {name}")
+    return name
+
+
+def code_object(source, name):
+    """hipRTC-compile (or fetch from the disk cache) a kernel's code object."""
+    key_src = "\n".join([source, _hip.device_header(), _arch(), str(_hip.rtc_version()),
+                         _hip.BACKEND_VERSION, " ".join(_hip.COMPILE_OPTIONS)])
+    key = hashlib.sha256(key_src.encode()).hexdigest()[:32]
+    path = os.path.join(_cache_dir(), f"{key}.hsaco")
+    if os.path.exists(path):
+        with open(path, "rb") as f:
+            return f.read()
+    try:
+        code = _hip.compile_hip(source, name, _arch())
+    except _hip.HIPRTCError as e:
+        lined = "\n".join(f"{i + 1:4d} | {ln}" for i, ln in enumerate(source.splitlines()))
+        raise _hip.HIPRTCError(f"{e}\n--- generated source ---\n{lined}") from None
+    tmp = f"{path}.{os.getpid()}.tmp"
+    with open(tmp, "wb") as f:
+        f.write(code)
+    os.replace(tmp, path)
+    with open(os.path.join(_cache_dir(), f"{key}.hip"), "w") as f:
+        f.write(source)
+    return code
+
+
+class CompiledKernel:
+    def __init__(self, name, source, lds_bytes, num_warps, params):
+        self.name = name
+        self.source = source
+        self.lds_bytes = lds_bytes
+        self.num_warps = num_warps
+        self.params = params  # list of (name, Param)
+        self.param_names = [n for n, _ in params]
+        self.kinds = []
+        for _, p in params:
+            if isinstance(p.dtype, tp.pointer_type):
+                self.kinds.append("ptr")
+            elif p.dtype == tp.int1:
+                self.kinds.append("bool")
+            elif p.dtype == tp.int64:
+                self.kinds.append("i64")
+            elif p.dtype.is_int:
+                self.kinds.append("i32")
+            else:
+                self.kinds.append("f32")
+        self.packer = _hip.pack_format(self.kinds)
+        self.code = code_object(source, name)
+        self.kernel = _hip.Kernel(self.code, name, lds_bytes)
+
+    def launch(self, grid, values, stream):
+        gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
+        self.kernel.launch_packed(gx, gy, gz, 64 * self.num_warps, stream,
+                                  self.packer.pack(*values))
+
+
+class JITFunction:
+    def __init__(self, fn):
+        functools.update_wrapper(self, fn)
+        self.fn = fn
+        src = textwrap.dedent(inspect.getsource(fn))
+        tree = ast.parse(src)
+        self.fndef = tree.body[0]
+        assert isinstance(self.fndef, ast.FunctionDef)
+        sig = inspect.signature(fn)
+        self.param_names = list(sig.parameters)
+        self.constexpr_names = [n for n, p in sig.parameters.items()
+                                if _is_constexpr_ann(p.annotation)]
+        self.defaults = {n: p.default for n, p in sig.parameters.items()
+                         if p.default is not inspect.Parameter.empty}
+        self.cache = {}
+
+    def __getitem__(self, grid):
+        return functools.partial(self._run, grid)
+
+    def __call__(self, *args, **kwargs):
+        raise RuntimeError(
+            f"@newt.jit kernel '{self.fn.__name__}' must be launched with a grid: "
+            f"kernel[grid](...)")
+
+    def _classify(self, args, kwargs):
+        """(constexprs, runtime values) from a call (reference jit.py:99-123)."""
+        if len(args) > len(self.param_names):
+            raise TypeError(f"{self.fn.__name__}() takes {len(self.param_names)} arguments "
+                            f"but {len(args)} were given")
+        bound = dict(zip(self.param_names, args))
+        for name, val in kwargs.items():
+            if name in self.param_names:
+                if name in bound:
+                    raise TypeError(f"duplicate argument {name}")
+                bound[name] = val
+        unknown = [k for k in kwargs if k not in self.param_names]
+        if unknown:
+            raise TypeError(f"unknown kernel arguments: {unknown}")
+        for name, d in self.defaults.items():
+            bound.setdefault(name, d)
+        missing = [n for n in self.param_names if n not in bound]
+        if missing:
+            raise TypeError(f"missing kernel arguments: {missing}")
+        constexprs = {n: bound[n] for n in self.constexpr_names}
+        runtime = {n: bound[n] for n in self.param_names if n not in self.constexpr_names}
+        return constexprs, runtime
+
+    @staticmethod
+    def _type_of(name, val):
+        """(dtype, specialization facts) of a runtime argument (reference jit.py:125-144)."""
+        import torch
+
+        if isinstance(val, torch.Tensor):
+            if not val.is_cuda:
+                raise TypeError(f"argument '{name}' must be a GPU tensor")
+            elem = tp.TORCH_TO_NEWT.get(str(val.dtype))
+            if elem is None:
+                raise TypeError(f"unsupported tensor dtype {val.dtype} for '{name}'")
+            return tp.pointer_type(elem), ("a16" if val.data_ptr() % 16 == 0 else "")
+        if isinstance(val, bool):
+            return tp.int1, ""
+        if isinstance(val, int):
+            if not -(2 ** 63) <= val < 2 ** 63:
+                raise TypeError(f"integer argument '{name}'={val} does not fit int64")
+            t = tp.int32 if -(2 ** 31) <= val < 2 ** 31 else tp.int64
+            return t, ("1" if val == 1 else f"d{_pow2_div(val)}")
+        if isinstance(val, float):
+            return tp.float32, ""
+        raise TypeError(f"unsupported kernel argument type {type(val)} for '{name}'")
+
+    def _compile(self, key, constexprs, runtime_types, num_warps, num_stages):
+        params = []
+        for name in self.param_names:
+            if name in self.constexpr_names:
+                continue
+            t, spec = runtime_types[name]
+            cname = f"g_{name}" if name in _CKEYWORDS else name
+            params.append((name, Param(t, cname, eq1=(spec == "1"),
+                                       div=int(spec[1:]) if spec.startswith("d") else 1,
+                                       aligned16=(spec == "a16"))))
+        khash = hashlib.sha256(repr(key).encode()).hexdigest()[:8]
+        kname = f"{self.fn.__name__}_{khash}"
+        source, lds = compile_fn(self.fndef, self.fn.__globals__, params, constexprs,
+                                 num_warps, kname, num_stages=num_stages)
+        if os.environ.get("NEWT_DEBUG"):
+            print(f"=== newt: {kname} (lds={lds}b, waves={num_warps}) ===")
+            print(source)
+        return CompiledKernel(kname, source, lds, num_warps, params)
+
+    def specialize(self, *args, num_warps=4, num_stages=3, **kwargs):
+        """Compile (without launching) for these arguments; returns the
+        CompiledKernel (source, code object, resource usage)."""
+        constexprs, runtime = self._classify(args, kwargs)
+        types = {n: self._type_of(n, v) for n, v in runtime.items()}
+        key = self._key(constexprs, types, num_warps, num_stages)
+        ck = self.cache.get(key)
+        if ck is None:
+            ck = self._compile(key, constexprs, types, num_warps, num_stages)
+            self.cache[key] = ck
+        return ck
+
+    @staticmethod
+    def _key(constexprs, types, num_warps, num_stages):
+        env = tuple(os.environ.get(k, "") for k in ("NEWT_VEC", "NEWT_PIPELINE_DOT",
+                                                    "NEWT_LDS_DMA", "NEWT_MFMA"))
+        return (tuple(sorted((k, repr(v)) for k, v in constexprs.items())),
+                tuple((n, t.name, s) for n, (t, s) in types.items()),
+                num_warps, num_stages, env)
+
+    def _run(self, grid, *args, **kwargs):
+        import torch
+
+        num_warps = kwargs.pop("num_warps", 4)
+        num_stages = kwargs.pop("num_stages", 3)
+        if num_warps not in (1, 2, 4, 8, 16):
+            raise ValueError(f"num_warps must be a power of two <= 16 (wave64s per "
+                             f"workgroup, at most 1024 threads), got {num_warps}")
+        if not 1 <= num_stages <= 8:
+            raise ValueError(f"num_stages must be in 1..8, got {num_stages}")
+        constexprs, runtime = self._classify(args, kwargs)
+        types = {n: self._type_of(n, v) for n, v in runtime.items()}
+        key = self._key(constexprs, types, num_warps, num_stages)
+        ck = self.cache.get(key)
+        if ck is None:
+            ck = self._compile(key, constexprs, types, num_warps, num_stages)
+            self.cache[key] = ck
+        values = []
+        dev = None
+        for name in ck.param_names:
+            v = runtime[name]
+            t = types[name][0]
+            if isinstance(t, tp.pointer_type):
+                if dev is None:
+                    dev = torch.cuda.current_device()
+                if v.device.index not in (None, dev):
+                    raise ValueError(
+                        f"tensor '{name}' is on {v.device} but the current device is "
+                        f"cuda:{dev}; newt launches on the current device")
+                values.append(v.data_ptr())
+            elif t == tp.float32:
+                values.append(float(v))
+            else:
+                values.append(v)
+        if callable(grid):
+            meta = dict(runtime)
+            meta.update(constexprs)
+            meta["num_warps"] = num_warps
+            g = grid(meta)
+        else:
+            g = grid
+        if isinstance(g, int):
+            g = (g,)
+        g = tuple(int(x) for x in g)
+        if any(x <= 0 for x in g):
+            return  # empty grid: no-op
+        stream = torch.cuda.current_stream().cuda_stream
+        ck.launch(g, values, stream)
+
+
+def jit(fn=None):
+    if fn is None:
+        return jit
+    return JITFunction(fn)

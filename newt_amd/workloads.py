@@ -1,0 +1,234 @@
+"""The five hot-path workloads written in the newt DSL, with host wrappers.
+
+These are user-level kernels exactly as a newt user writes them (the
+reference's examples/01-05), extended to the BASELINE configurations:
+  add_kernel        examples/01_vector_add.py:14-21 (unchanged)
+  softmax_kernel    examples/02_fused_softmax.py:15-24 (unchanged)
+  layernorm_kernel  examples/03_layernorm.py:13-27 + stores of the saved
+                    per-row mean / rstd (config 3 asks for them)
+  matmul_kernel     examples/04_matmul.py:14-45 (unchanged body), autotuned over
+                    a configuration space re-derived for gfx950
+  attention_kernel  examples/05_fused_attention.py:14-48 generalised to
+                    [batch, heads, seq, head_dim] with a batch*head grid axis,
+                    strides, an optional causal mask with the loop bound trimmed
+                    to the diagonal, and p cast to V's dtype before P @ V
+Everything is compiled by newt_amd's compiler to HIP for gfx950.
+"""
+
+import torch
+
+import newt_amd as newt
+import newt_amd.language as nl
+
+
+# ---------------------------------------------------------------------------
+# 1. vector add
+# ---------------------------------------------------------------------------
+@newt.jit
+def add_kernel(x_ptr, y_ptr, out_ptr, n, BLOCK: nl.constexpr):
+    pid = nl.program_id(0)
+    offs = pid * BLOCK + nl.arange(0, BLOCK)
+    mask = offs < n
+    x = nl.load(x_ptr + offs, mask=mask)
+    y = nl.load(y_ptr + offs, mask=mask)
+    nl.store(out_ptr + offs, x + y, mask=mask)
+
+
+def add(x, y, out=None, BLOCK=1024, num_warps=4):
+    out = torch.empty_like(x) if out is None else out
+    n = x.numel()
+    add_kernel[(newt.cdiv(n, BLOCK),)](x, y, out, n, BLOCK=BLOCK, num_warps=num_warps)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# 2. fused row softmax
+# ---------------------------------------------------------------------------
+@newt.jit
+def softmax_kernel(x_ptr, out_ptr, N, stride, BLOCK_N: nl.constexpr):
+    row = nl.program_id(0)
+    cols = nl.arange(0, BLOCK_N)
+    mask = cols < N
+    x = nl.load(x_ptr + row * stride + cols, mask=mask, other=float("-inf"))
+    x = x - nl.max(x, axis=0)
+    num = nl.exp(x)
+    den = nl.sum(num, axis=0)
+    nl.store(out_ptr + row * stride + cols, num / den, mask=mask)
+
+
+def softmax_warps(block_n):
+    # one row per workgroup; 8-16 fp32 values per thread
+    return max(1, min(16, block_n // 512))
+
+
+def softmax(x, out=None, num_warps=None):
+    M, N = x.shape
+    out = torch.empty_like(x) if out is None else out
+    BLOCK_N = newt.next_power_of_2(N)
+    nw = num_warps or softmax_warps(BLOCK_N)
+    softmax_kernel[(M,)](x, out, N, x.stride(0), BLOCK_N=BLOCK_N, num_warps=nw)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# 3. layernorm forward (+ saved mean / rstd)
+# ---------------------------------------------------------------------------
+@newt.jit
+def layernorm_kernel(x_ptr, w_ptr, b_ptr, out_ptr, mean_ptr, rstd_ptr, N, stride, eps,
+                     BLOCK_N: nl.constexpr):
+    row = nl.program_id(0)
+    cols = nl.arange(0, BLOCK_N)
+    mask = cols < N
+    x = nl.load(x_ptr + row * stride + cols, mask=mask, other=0.0)
+    mean = nl.sum(x, axis=0) / N
+    diff = nl.where(mask, x - mean, 0.0)
+    var = nl.sum(diff * diff, axis=0) / N
+    rstd = nl.rsqrt(var + eps)
+    w = nl.load(w_ptr + cols, mask=mask)
+    b = nl.load(b_ptr + cols, mask=mask)
+    y = (x - mean) * rstd * w + b
+    nl.store(out_ptr + row * stride + cols, y, mask=mask)
+    nl.store(mean_ptr + row, mean)
+    nl.store(rstd_ptr + row, rstd)
+
+
+def layernorm(x, w, b, eps=1e-5, out=None, num_warps=None):
+    M, N = x.shape
+    out = torch.empty_like(x) if out is None else out
+    mean = torch.empty(M, device=x.device, dtype=torch.float32)
+    rstd = torch.empty(M, device=x.device, dtype=torch.float32)
+    BLOCK_N = newt.next_power_of_2(N)
+    nw = num_warps or max(1, min(16, BLOCK_N // 1024))
+    layernorm_kernel[(M,)](x, w, b, out, mean, rstd, N, x.stride(0), eps,
+                           BLOCK_N=BLOCK_N, num_warps=nw)
+    return out, mean, rstd
+
+
+# ---------------------------------------------------------------------------
+# 4. matmul (fp16 / bf16, fp32 accumulate)
+# ---------------------------------------------------------------------------
+@newt.jit
+def matmul_kernel(a_ptr, b_ptr, c_ptr, M, N, K,
+                  sam, sak, sbk, sbn, scm, scn,
+                  BLOCK_M: nl.constexpr, BLOCK_N: nl.constexpr, BLOCK_K: nl.constexpr):
+    pid_m = nl.program_id(0)
+    pid_n = nl.program_id(1)
+    offs_m = pid_m * BLOCK_M + nl.arange(0, BLOCK_M)
+    offs_n = pid_n * BLOCK_N + nl.arange(0, BLOCK_N)
+    offs_k = nl.arange(0, BLOCK_K)
+    a_ptrs = a_ptr + offs_m[:, None] * sam + offs_k[None, :] * sak
+    b_ptrs = b_ptr + offs_k[:, None] * sbk + offs_n[None, :] * sbn
+    acc = nl.zeros((BLOCK_M, BLOCK_N), dtype=nl.float32)
+    for k in range(nl.cdiv(K, BLOCK_K)):
+        a_mask = (offs_m[:, None] < M) & (offs_k[None, :] < K - k * BLOCK_K)
+        b_mask = (offs_k[:, None] < K - k * BLOCK_K) & (offs_n[None, :] < N)
+        a = nl.load(a_ptrs, mask=a_mask, other=0.0)
+        b = nl.load(b_ptrs, mask=b_mask, other=0.0)
+        acc = nl.dot(a, b, acc)
+        a_ptrs += BLOCK_K * sak
+        b_ptrs += BLOCK_K * sbk
+    c_ptrs = c_ptr + offs_m[:, None] * scm + offs_n[None, :] * scn
+    c_mask = (offs_m[:, None] < M) & (offs_n[None, :] < N)
+    nl.store(c_ptrs, acc.to(c_ptr.dtype.element_ty), mask=c_mask)
+
+
+# gfx950 search space: 64-wide waves, 160 KB LDS per CU, 256 CUs. Tiles of
+# 128-256 keep the 4096^3 grid at 256-1024 workgroups (>= one per CU); BLOCK_K
+# 32/64 with 2-3 LDS stages fit the LDS budget.
+MATMUL_CONFIGS = [
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 64}, num_warps=8, num_stages=2),
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=8, num_stages=3),
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=8, num_stages=2),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 256, "BLOCK_K": 64}, num_warps=8, num_stages=2),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=2),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=4, num_stages=3),
+    newt.Config({"BLOCK_M": 64, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=2),
+    newt.Config({"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 64}, num_warps=4, num_stages=2),
+]
+
+matmul_tuned = newt.autotune(configs=MATMUL_CONFIGS, key=["M", "N", "K"])(matmul_kernel)
+
+
+def matmul(a, b, c=None, config=None):
+    M, K = a.shape
+    K2, N = b.shape
+    assert K == K2
+    c = torch.empty(M, N, device=a.device, dtype=a.dtype) if c is None else c
+    args = (a, b, c, M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
+            c.stride(0), c.stride(1))
+    if config is None:
+        grid = lambda meta: (newt.cdiv(M, meta["BLOCK_M"]), newt.cdiv(N, meta["BLOCK_N"]))
+        matmul_tuned[grid](*args)
+    else:
+        grid = (newt.cdiv(M, config.kwargs["BLOCK_M"]), newt.cdiv(N, config.kwargs["BLOCK_N"]))
+        matmul_kernel[grid](*args, **config.kwargs, num_warps=config.num_warps,
+                            num_stages=config.num_stages)
+    return c
+
+
+# ---------------------------------------------------------------------------
+# 5. flash attention forward
+# ---------------------------------------------------------------------------
+@newt.jit
+def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
+                     sqb, sqh, sqm, skb, skh, skn, svb, svh, svn, sob, soh, som,
+                     BLOCK_M: nl.constexpr, BLOCK_N: nl.constexpr, D: nl.constexpr,
+                     CAUSAL: nl.constexpr):
+    pid = nl.program_id(0)
+    bh = nl.program_id(1)
+    bi = bh // H
+    hi = bh % H
+    q_base = q_ptr + bi * sqb + hi * sqh
+    k_base = k_ptr + bi * skb + hi * skh
+    v_base = v_ptr + bi * svb + hi * svh
+    o_base = o_ptr + bi * sob + hi * soh
+    offs_m = pid * BLOCK_M + nl.arange(0, BLOCK_M)
+    offs_d = nl.arange(0, D)
+    qmask = offs_m[:, None] < S
+    q = nl.load(q_base + offs_m[:, None] * sqm + offs_d[None, :], mask=qmask, other=0.0)
+
+    m_i = nl.full((BLOCK_M,), float("-inf"), dtype=nl.float32)
+    l_i = nl.zeros((BLOCK_M,), dtype=nl.float32)
+    acc = nl.zeros((BLOCK_M, D), dtype=nl.float32)
+
+    end_n = S
+    if CAUSAL:
+        end_n = nl.minimum(S, (pid + 1) * BLOCK_M)
+    for start_n in range(0, end_n, BLOCK_N):
+        offs_n = start_n + nl.arange(0, BLOCK_N)
+        nmask = offs_n[:, None] < S
+        k = nl.load(k_base + offs_n[:, None] * skn + offs_d[None, :], mask=nmask, other=0.0)
+        qk = nl.dot(q, nl.trans(k)) * scale
+        if CAUSAL:
+            qk = nl.where((offs_m[:, None] >= offs_n[None, :]) & (offs_n[None, :] < S),
+                          qk, float("-inf"))
+        else:
+            qk = nl.where(offs_n[None, :] < S, qk, float("-inf"))
+        m_new = nl.maximum(m_i, nl.max(qk, axis=1))
+        alpha = nl.exp(m_i - m_new)
+        p = nl.exp(qk - m_new[:, None])
+        l_i = l_i * alpha + nl.sum(p, axis=1)
+        acc = acc * alpha[:, None]
+        v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :], mask=nmask, other=0.0)
+        acc = nl.dot(p.to(v_ptr.dtype.element_ty), v, acc)
+        m_i = m_new
+
+    acc = acc / l_i[:, None]
+    nl.store(o_base + offs_m[:, None] * som + offs_d[None, :], acc.to(o_ptr.dtype.element_ty),
+             mask=qmask)
+
+
+def attention(q, k, v, causal=False, scale=None, out=None, BLOCK_M=128, BLOCK_N=64,
+              num_warps=4, num_stages=2):
+    B, H, S, D = q.shape
+    out = torch.empty_like(q) if out is None else out
+    scale = D ** -0.5 if scale is None else scale
+    grid = (newt.cdiv(S, BLOCK_M), B * H)
+    attention_kernel[grid](q, k, v, out, S, H, scale,
+                           q.stride(0), q.stride(1), q.stride(2),
+                           k.stride(0), k.stride(1), k.stride(2),
+                           v.stride(0), v.stride(1), v.stride(2),
+                           out.stride(0), out.stride(1), out.stride(2),
+                           BLOCK_M=BLOCK_M, BLOCK_N=BLOCK_N, D=D, CAUSAL=causal,
+                           num_warps=num_warps, num_stages=num_stages)
+    return out

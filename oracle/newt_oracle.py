@@ -1,0 +1,138 @@
+"""CPU oracle for the newt hot path - TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only as the checker (or as the timed CPU baseline). No product
+code path calls it; the HIP extension failing to load is an error, never a
+fallback to this file.
+
+Each function restates, in numpy, the algorithm of one kernel the reference
+runs on the GPU, in the arithmetic the reference specifies:
+
+  vector_add      examples/01_vector_add.py:14-21      out = x + y (fp32, exact)
+  softmax_rows    examples/02_fused_softmax.py:15-24   exp(x - rowmax) / rowsum, fp32
+  layernorm_rows  examples/03_layernorm.py:13-27       two-pass mean/var, fp32 math,
+                                                       output cast to x.dtype,
+                                                       plus saved mean / rstd
+  matmul          examples/04_matmul.py:14-45          fp32 accumulation of the
+                                                       fp16/bf16 products, cast to C dtype
+  attention       examples/05_fused_attention.py:14-48 softmax(q k^T * scale [+ causal
+                                                       mask]) v with fp32 softmax state,
+                                                       P rounded to the value dtype
+                                                       before P @ V, output in q.dtype
+
+Pinning (tests/test_oracle.py): every function is checked against the golden
+fixtures in tests/golden (written by torch eager in float64 - the reference's
+own oracle), against closed forms (softmax of a constant row, rows summing to
+1, layernorm output moments, attention with identical keys returning the mean
+of V, causal row 0 returning v[0]) and against brute-force loops on tiny
+inputs, so that a dropped term, wrong axis or transposed operand fails.
+"""
+
+import numpy as np
+
+def round_bf16(x):
+    """Round float32 values to bfloat16 (round-to-nearest-even), return float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(x)
+    lsb = (u >> 16) & 1
+    u = (u + 0x7FFF + lsb) & 0xFFFF0000
+    out = u.astype(np.uint32).view(np.float32)
+    out = np.where(nan, np.float32(np.nan), out)
+    return out
+
+
+def round_to(x, dtype):
+    """Round float32 values to `dtype` ('float32' | 'float16' | 'bfloat16')."""
+    x = np.asarray(x, dtype=np.float32)
+    if dtype == "float16":
+        return x.astype(np.float16).astype(np.float32)
+    if dtype == "bfloat16":
+        return round_bf16(x)
+    return x
+
+
+def vector_add(x, y):
+    """examples/01_vector_add.py:14-21: elementwise IEEE fp32 add."""
+    return (np.asarray(x, np.float32) + np.asarray(y, np.float32)).astype(np.float32)
+
+
+def softmax_rows(x):
+    """examples/02_fused_softmax.py:15-24: row max, exp(x - max), row sum, divide.
+    fp32 throughout (float64 intermediate exp for a tight reference)."""
+    x = np.asarray(x, np.float32)
+    m = x.max(axis=1, keepdims=True)
+    e = np.exp((x - m).astype(np.float64))
+    return (e / e.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def layernorm_rows(x, w, b, eps=1e-5, out_dtype="float32"):
+    """examples/03_layernorm.py:13-27 (two-pass: mean, then mean of squared
+    deviations), fp32 math on upcast inputs; returns (y, mean, rstd) with y
+    rounded to out_dtype and mean/rstd in fp32."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    b = np.asarray(b, np.float64)
+    n = x.shape[1]
+    mean = x.sum(axis=1) / n
+    diff = x - mean[:, None]
+    var = (diff * diff).sum(axis=1) / n
+    rstd = 1.0 / np.sqrt(var + eps)
+    y = diff * rstd[:, None] * w[None, :] + b[None, :]
+    return (round_to(y.astype(np.float32), out_dtype), mean.astype(np.float32),
+            rstd.astype(np.float32))
+
+
+def matmul(a, b, out_dtype="float32"):
+    """examples/04_matmul.py:14-45: C = A @ B with fp32 (here fp64) accumulation
+    of the (already fp16/bf16-valued) inputs, rounded to the C dtype."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return round_to((a @ b).astype(np.float32), out_dtype)
+
+
+def attention(q, k, v, scale, causal=False, p_dtype=None, out_dtype="float32"):
+    """examples/05_fused_attention.py:14-48 generalised to [B, H, S, D]:
+    S = q k^T * scale, optional causal mask (key index <= query index),
+    P = softmax(S) (fp32 state), P rounded to the value dtype before P @ V
+    (the reference casts p to the MMA dtype), O = P V / rowsum.
+    The normalisation uses the unrounded row sums, as the online-softmax
+    kernel accumulates l_i from the fp32 probabilities."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    s = np.einsum("...md,...nd->...mn", q, k) * scale
+    if causal:
+        M, N = s.shape[-2:]
+        keep = np.arange(N)[None, :] <= np.arange(M)[:, None]
+        s = np.where(keep, s, -np.inf)
+    m = s.max(axis=-1, keepdims=True)
+    p = np.exp(s - m)
+    l = p.sum(axis=-1, keepdims=True)
+    if p_dtype is not None:
+        p = round_to(p.astype(np.float32), p_dtype).astype(np.float64)
+    o = np.einsum("...mn,...nd->...md", p, v) / l
+    return round_to(o.astype(np.float32), out_dtype)
+
+
+def rel_frobenius(actual, expected):
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    return float(np.linalg.norm(a - e) / max(np.linalg.norm(e), 1e-30))
+
+
+# -- brute-force forms for tiny inputs (pinning helpers) -------------------------
+
+def matmul_loops(a, b):
+    M, K = len(a), len(a[0])
+    N = len(b[0])
+    return [[sum(float(a[i][kk]) * float(b[kk][j]) for kk in range(K)) for j in range(N)]
+            for i in range(M)]
+
+
+def softmax_loops(row):
+    import math
+    m = max(row)
+    e = [math.exp(v - m) for v in row]
+    s = sum(e)
+    return [v / s for v in e]

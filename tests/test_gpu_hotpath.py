@@ -1,0 +1,145 @@
+"""Parity of the five hot-path kernels on the GPU against the CPU oracle.
+
+Each test runs the newt kernel through the HIP backend (hipRTC code object
+launched through libnewt_hip.so) on seeded inputs and compares with
+oracle/newt_oracle.py at the tolerance north_star states:
+  vector add (elementwise): bit-exact
+  softmax fp32: rtol 1e-5; layernorm fp16 output: 2e-3 (mean/rstd fp32: 1e-5)
+  matmul, attention (fp16/bf16): relative Frobenius error <= 1e-2
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import newt_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def seeded(shape, seed, scale=1.0, mean=0.0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale + mean).to(dtype).to("cuda")
+
+
+def npf(t):
+    return t.detach().float().cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def W():
+    from newt_amd import workloads
+    return workloads
+
+
+@pytest.mark.parametrize("n", [1024, 1 << 20, 12345, 1_000_000, 1])
+def test_vector_add_bit_exact(W, n):
+    x, y = seeded(n, 0), seeded(n, 1)
+    out = W.add(x, y)
+    torch.cuda.synchronize()
+    ref = orc.vector_add(npf(x), npf(y))
+    assert np.array_equal(npf(out), ref), f"n={n}"
+
+
+def test_vector_add_golden(W):
+    g = np.load("tests/golden/vector_add_12345.npz")
+    x = torch.from_numpy(g["x"]).cuda()
+    y = torch.from_numpy(g["y"]).cuda()
+    out = W.add(x, y)
+    assert np.array_equal(npf(out), g["out"])
+
+
+@pytest.mark.parametrize("M,N", [(8, 128), (128, 1024), (32, 781), (64, 1000), (16, 4096),
+                                 (4, 8192), (3, 5)])
+def test_softmax(W, M, N):
+    x = seeded((M, N), 0, scale=4.0)
+    out = W.softmax(x)
+    ref = orc.softmax_rows(npf(x))
+    np.testing.assert_allclose(npf(out), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_softmax_golden(W):
+    for name in ("softmax_8x128", "softmax_32x781"):
+        g = np.load(f"tests/golden/{name}.npz")
+        out = W.softmax(torch.from_numpy(g["x"]).cuda())
+        np.testing.assert_allclose(npf(out), g["out"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("M,N", [(8, 128), (16, 300), (64, 2048), (4, 8192), (2, 1000)])
+def test_layernorm_fp16(W, M, N):
+    x = seeded((M, N), 0, dtype=torch.float16)
+    w = seeded(N, 2, scale=0.1, mean=1.0, dtype=torch.float16)
+    b = seeded(N, 3, scale=0.1, dtype=torch.float16)
+    y, mean, rstd = W.layernorm(x, w, b, 1e-5)
+    ry, rmean, rrstd = orc.layernorm_rows(npf(x), npf(w), npf(b), 1e-5, "float16")
+    np.testing.assert_allclose(npf(y), ry, rtol=2e-3, atol=2e-3)
+    np.testing.assert_allclose(npf(mean), rmean, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(npf(rstd), rrstd, rtol=1e-5, atol=1e-6)
+
+
+def test_layernorm_fp32(W):
+    M, N = 16, 3000
+    x = seeded((M, N), 0)
+    w = seeded(N, 2)
+    b = seeded(N, 3)
+    y, mean, rstd = W.layernorm(x, w, b, 1e-5)
+    ry, rmean, rrstd = orc.layernorm_rows(npf(x), npf(w), npf(b), 1e-5, "float32")
+    np.testing.assert_allclose(npf(y), ry, rtol=1e-5, atol=1e-5)
+
+
+def test_layernorm_golden(W):
+    for name in ("layernorm_16x300", "layernorm_8x128"):
+        g = np.load(f"tests/golden/{name}.npz")
+        t = lambda k: torch.from_numpy(g[k]).half().cuda()
+        y, mean, rstd = W.layernorm(t("x"), t("w"), t("b"), 1e-5)
+        np.testing.assert_allclose(npf(y), g["out"], rtol=2e-3, atol=2e-3)
+        np.testing.assert_allclose(npf(mean), g["mean"], rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(npf(rstd), g["rstd"], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K,cfg", [
+    (64, 64, 32, (64, 64, 32, 4, 2)),
+    (256, 256, 128, (64, 64, 32, 4, 2)),
+    (300, 200, 100, (64, 64, 32, 4, 2)),
+    (512, 512, 256, (128, 128, 64, 4, 2)),
+    (512, 384, 512, (256, 128, 64, 8, 2)),
+])
+def test_matmul(W, dtype, M, N, K, cfg):
+    import newt_amd as newt
+    a = seeded((M, K), 4, scale=K ** -0.5, dtype=dtype)
+    b = seeded((K, N), 5, scale=K ** -0.5, dtype=dtype)
+    BM, BN, BK, nw, ns = cfg
+    c = W.matmul(a, b, config=newt.Config({"BLOCK_M": BM, "BLOCK_N": BN, "BLOCK_K": BK},
+                                         num_warps=nw, num_stages=ns))
+    ref = orc.matmul(npf(a), npf(b), "float16" if dtype == torch.float16 else "bfloat16")
+    assert orc.rel_frobenius(npf(c), ref) <= 1e-2
+
+
+def test_matmul_golden(W):
+    import newt_amd as newt
+    cfg = newt.Config({"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 32}, num_warps=4, num_stages=2)
+    for name in ("matmul_64x64x32", "matmul_300x200x100"):
+        g = np.load(f"tests/golden/{name}.npz")
+        a = torch.from_numpy(g["a"]).half().cuda()
+        b = torch.from_numpy(g["b"]).half().cuda()
+        c = W.matmul(a, b, config=cfg)
+        assert orc.rel_frobenius(npf(c), g["out"]) <= 1e-2
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,S,D", [(1, 2, 64, 32), (1, 2, 256, 64), (2, 2, 200, 128)])
+def test_attention(W, causal, B, H, S, D):
+    q, k, v = (seeded((B, H, S, D), s, dtype=torch.bfloat16) for s in (6, 7, 8))
+    o = W.attention(q, k, v, causal=causal, BLOCK_M=64, BLOCK_N=64, num_warps=4)
+    ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    assert orc.rel_frobenius(npf(o), ref) <= 1e-2
+
+
+def test_attention_golden(W):
+    for causal in (False, True):
+        g = np.load(f"tests/golden/attention_1x2x64x32_{'causal' if causal else 'full'}.npz")
+        t = lambda k: torch.from_numpy(g[k]).bfloat16().cuda()
+        o = W.attention(t("q"), t("k"), t("v"), causal=causal, BLOCK_M=64, BLOCK_N=64)
+        assert orc.rel_frobenius(npf(o), g["out"]) <= 1e-2
