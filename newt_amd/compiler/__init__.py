@@ -42,7 +42,7 @@ def _has_row_reduction(fndef):
 
 
 def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, num_stages=3,
-               max_passes=6):
+               max_passes=10):
     """Compile a kernel. Returns (hip_source, lds_bytes).
 
     params: list of (name, Param) for the runtime parameters in signature order.

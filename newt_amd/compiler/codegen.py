@@ -147,6 +147,8 @@ class Codegen(ast.NodeVisitor):
         self.pending_hoist = []
         self.body_stack = []
         self.dot_state = {}
+        self.lds_arrays = []      # (name, bytes): distinct __shared__ arrays (pipeline stages)
+        self.pipe_records = []
         self.params = params
         vec = 1
         for _, p in params:
@@ -625,8 +627,19 @@ class Codegen(ast.NodeVisitor):
         lds_total = self.lds_dedicated
         arena_off = (lds_total + 15) // 16 * 16
         lds_total = arena_off + self.arena_bytes
-        if lds_total > MAX_LDS:
-            raise CompileError(f"kernel needs {lds_total} bytes of LDS (max {MAX_LDS}); "
+        lds_all = lds_total + sum(b for _, b in self.lds_arrays)
+        if lds_all > MAX_LDS:
+            # a dot pipeline that does not fit gives up a stage (down to 2), then
+            # falls back to synchronous staging, before the kernel is rejected
+            for rec in self.pipe_records:
+                key = rec["node"].lineno
+                if rec["S"] > 2:
+                    self.new_hints[("pipe_stages", key)] = rec["S"] - 1
+                    raise _Retry()
+                if not self.hints.get(("nopipe", key)):
+                    self.new_hints[("nopipe", key)] = True
+                    raise _Retry()
+            raise CompileError(f"kernel needs {lds_all} bytes of LDS (max {MAX_LDS}); "
                                f"use smaller block sizes")
         sig = []
         for name, p in self.params:
@@ -643,15 +656,17 @@ class Codegen(ast.NodeVisitor):
                    f'{self.name}({", ".join(sig)}) {{')
         if lds_total:
             out.append(f"  __shared__ __attribute__((aligned(16))) unsigned char _lds[{lds_total}];")
+        for nm, nb in self.lds_arrays:
+            out.append(f"  __shared__ __attribute__((aligned(16))) unsigned char {nm}[{nb}];")
         out.append("  const int _tid = (int)threadIdx.x;")
         out.append("  const int _lane = _tid & 63;")
-        out.append("  const int _wave = _tid >> 6;")
+        out.append("  const int _wave = __builtin_amdgcn_readfirstlane(_tid >> 6);")
         out.append("  (void)_lane; (void)_wave;")
         for p in self.prologue:
             out.append("  " + p)
         out += self.lines
         out.append("}")
-        self.lds_total = lds_total
+        self.lds_total = lds_all
         return "\n".join(out) + "\n"
 
     # -------------------------------------------------------------- statements
@@ -775,6 +790,10 @@ class Codegen(ast.NodeVisitor):
             if not isinstance(a, (Const, Scalar)):
                 self.err(node, "range bounds must be scalars")
         idt = tp.int64 if any(self.cdtype(a) == tp.int64 for a in (lo_, hi, st)) else tp.int32
+        if isinstance(st, Const) and isinstance(st.pyval, int) and st.pyval > 0:
+            plan = self.pipeline_plan(node)
+            if plan is not None:
+                return self.pipelined_for(node, plan, lo_, hi, st, idt)
         rec = self._enter_compound(node)
         self.drain_dots_for_loop(node)
         ivar = self.fresh("i")

@@ -249,4 +249,95 @@ __device__ __forceinline__ void lds_read(const T* base, int off, T* out) {
   load_vec<T, N>(base + off, out);
 }
 
+// Inverse of LdsTile::off at 16-byte granularity: the (row, first k) whose
+// chunk sits in physical chunk `slot` of the tile (used to aim direct-to-LDS
+// loads, whose destination is fixed by the lane index).
+template <typename T, int KD>
+__device__ __forceinline__ void lds_tile_slot(int slot, int& r, int& k) {
+  typedef LdsTile<T, KD> L;
+  r = slot / L::CPR;
+  k = ((slot % L::CPR) ^ ((r >> L::SHIFT) & L::SWZ)) * L::EPC;
+}
+
+// ---------------------------------------------------------------------------
+// LDS operand tiles stored with the ROW index contiguous: a [KD][RD] array of
+// 16-bit elements (RD = rows of the [R, K] operand view, RD >= 32). This is how
+// an operand whose rows are contiguous in global memory (B of a row-major
+// A @ B) lands in LDS with plain 16-byte writes; fragments are read back
+// transposed with ds_read_b64_tr_b16. 64-byte units of a k-row are XOR
+// swizzled so the four k-rows one transposed read touches fall in four
+// different 64-byte quarters of the 64 banks.
+// ---------------------------------------------------------------------------
+template <typename T, int RD>
+struct LdsTileR {
+  static_assert(sizeof(T) == 2 && RD >= 32 && RD % 32 == 0, "R-major tiles hold >= 32 16-bit rows");
+  static constexpr int ROW_BYTES = RD * 2;
+  __device__ __forceinline__ static int swz(int k) {
+    if constexpr (ROW_BYTES >= 256) return k & 3;
+    else if constexpr (ROW_BYTES == 128) return (k >> 1) & 1;
+    else return 0;
+  }
+  __device__ __forceinline__ static int off(int k, int r) {
+    return k * RD + (((r >> 5) ^ swz(k)) << 5) + (r & 31);
+  }
+  // (k, first r) of the 8-element chunk at physical chunk index `slot`
+  __device__ __forceinline__ static void slot(int s, int& k, int& r) {
+    k = s / (RD / 8);
+    const int pe = (s % (RD / 8)) * 8;
+    r = (((pe >> 5) ^ swz(k)) << 5) | (pe & 31);
+  }
+};
+
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// One MFMA operand fragment (8 consecutive k of one operand row per lane) from
+// an R-major tile. MI is the instruction's row tile (32 or 16): lane l gets
+// row r0 + (l % MI) and k = kk + 8 * (l / MI) + 0..7. Each ds_read_b64_tr_b16
+// lets a group of 16 lanes read a 4(k) x 16(r) sub-block and hands lane i the
+// four k values of row (group base + i).
+template <typename T, int RD, int MI>
+__device__ __forceinline__ i16x8 lds_frag_r(const T* tile, int r0, int kk, int lane) {
+  typedef LdsTileR<T, RD> L;
+  const int i = lane & 15;
+  const int cb = r0 + ((lane & (MI - 1)) & ~15) + 4 * (i & 3);
+  const int kr = kk + 8 * (lane / MI) + (i >> 2);
+  const __attribute__((address_space(3))) char* b =
+      (const __attribute__((address_space(3))) char*)tile;
+  i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(b + 2 * L::off(kr, cb)));
+  i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(b + 2 * L::off(kr + 4, cb)));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Fragment of a K-major tile (LdsTile): lane l gets row r0 + (l % MI) and
+// k = kk + 8 * (l / MI) + 0..7 as one ds_read_b128.
+template <typename T, int KD, int MI>
+__device__ __forceinline__ i16x8 lds_frag_k(const T* tile, int r0, int kk, int lane) {
+  return *(const i16x8*)(tile + LdsTile<T, KD>::off(r0 + (lane & (MI - 1)), kk + 8 * (lane / MI)));
+}
+
+// Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4):
+// lane l's 16 bytes land at wave_dst + 16 * l. wave_dst must be the same for
+// every lane of the wave.
+__device__ __forceinline__ void lds_dma16(const void* g, void* wave_dst) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)wave_dst, 16, 0, 0);
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (s_waitcnt vmcnt(N); expcnt and lgkmcnt left unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+template <typename T> struct frag8;
+template <> struct frag8<f16> { typedef f16x8 type; };
+template <> struct frag8<bf16> { typedef bf16x8 type; };
+
+template <typename T>
+__device__ __forceinline__ typename frag8<T>::type as_frag(i16x8 v) {
+  return __builtin_bit_cast(typename frag8<T>::type, v);
+}
+
 }  // namespace newt

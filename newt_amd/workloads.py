@@ -132,18 +132,20 @@ def matmul_kernel(a_ptr, b_ptr, c_ptr, M, N, K,
     nl.store(c_ptrs, acc.to(c_ptr.dtype.element_ty), mask=c_mask)
 
 
-# gfx950 search space: 64-wide waves, 160 KB LDS per CU, 256 CUs. Tiles of
-# 128-256 keep the 4096^3 grid at 256-1024 workgroups (>= one per CU); BLOCK_K
-# 32/64 with 2-3 LDS stages fit the LDS budget.
+# gfx950 search space: 64-wide waves, 160 KB LDS per CU, 256 CUs. The k-loop is
+# software-pipelined num_stages deep through distinct LDS stages, so tiles of
+# 256x256 with BLOCK_K=32 and 4 stages (128 KB) give each CU one 8-wave
+# workgroup with a 128x64 MFMA sub-tile per wave; smaller tiles keep grids of
+# >= 256 workgroups for smaller problems.
 MATMUL_CONFIGS = [
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=8, num_stages=4),
     newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 64}, num_warps=8, num_stages=2),
     newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=8, num_stages=3),
-    newt.Config({"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=8, num_stages=2),
-    newt.Config({"BLOCK_M": 128, "BLOCK_N": 256, "BLOCK_K": 64}, num_warps=8, num_stages=2),
-    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=2),
-    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=4, num_stages=3),
-    newt.Config({"BLOCK_M": 64, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=2),
-    newt.Config({"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 64}, num_warps=4, num_stages=2),
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=8, num_stages=4),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=8, num_stages=4),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=3),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=4, num_stages=4),
+    newt.Config({"BLOCK_M": 64, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=3),
 ]
 
 matmul_tuned = newt.autotune(configs=MATMUL_CONFIGS, key=["M", "N", "K"])(matmul_kernel)

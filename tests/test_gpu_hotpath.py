@@ -116,6 +116,25 @@ def test_matmul(W, dtype, M, N, K, cfg):
     assert orc.rel_frobenius(npf(c), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (300, 200, 100), (256, 256, 64),
+                                   (1024, 768, 1056), (64, 96, 32), (520, 264, 136)])
+@pytest.mark.parametrize("cfg", [(256, 256, 32, 8, 4), (128, 128, 32, 4, 3), (64, 64, 32, 4, 4),
+                                 (128, 256, 64, 8, 2)])
+def test_matmul_pipelined(W, dtype, M, N, K, cfg):
+    """The software-pipelined k-loop (direct-to-LDS stages, ragged fallbacks,
+    trip counts shorter than the pipeline) against the oracle."""
+    import newt_amd as newt
+    a = seeded((M, K), 4, scale=K ** -0.5, dtype=dtype)
+    b = seeded((K, N), 5, scale=K ** -0.5, dtype=dtype)
+    BM, BN, BK, nw, ns = cfg
+    print(f"matmul_pipelined M={M} N={N} K={K} cfg={cfg} {dtype}", flush=True)
+    c = W.matmul(a, b, config=newt.Config({"BLOCK_M": BM, "BLOCK_N": BN, "BLOCK_K": BK},
+                                         num_warps=nw, num_stages=ns))
+    ref = orc.matmul(npf(a), npf(b), "float16" if dtype == torch.float16 else "bfloat16")
+    assert orc.rel_frobenius(npf(c), ref) <= 1e-2
+
+
 def test_matmul_golden(W):
     import newt_amd as newt
     cfg = newt.Config({"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 32}, num_warps=4, num_stages=2)
