@@ -930,8 +930,9 @@ class Codegen(ast.NodeVisitor):
             else:
                 L = self.default_layout(v.shape)
             vec = 0
-            if L.tag.startswith("mfma") and not L.tag.startswith("mfmaop") and v.dtype == tp.float32:
-                vec = 16 if "32x32" in L.tag else 4
+            mi = lo.mfma_tag_instr(L.tag)
+            if mi is not None and v.dtype == tp.float32:
+                vec = lo.INSTR[mi[0]][4]
             if vec:
                 vt = {16: "f32x16", 4: "f32x4"}[vec]
                 emit_decl(f"{vt} {cvar}[{L.nslots // vec}];")

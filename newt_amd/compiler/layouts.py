@@ -298,26 +298,31 @@ INSTR = {
 }
 
 
-def mfma_c(M, N, instr, wm, wn):
+def mfma_c(M, N, instr, wm, wn, orient="row"):
     """Accumulator layout of an [M, N] dot result computed by a wm x wn grid of
-    waves, each owning an (M/wm) x (N/wn) sub-tile of instr tiles."""
+    waves, each owning an (M/wm) x (N/wn) sub-tile of instr tiles.
+
+    orient="row": the MFMA computes C^T = B^T A^T, so a lane holds (part of)
+    one ROW of C and registers walk columns - row reductions stay in-lane.
+    orient="col": the MFMA computes C = A B directly, a lane holds part of one
+    COLUMN and registers walk rows (tag suffix "c")."""
     MI, NI, KI, kpl, nacc = INSTR[instr]
     assert MI == NI
-    rb = log2i(MI)  # row bits covered by one instruction tile (5 or 4)
+    rb = log2i(MI)  # bits covered by one instruction tile along the lane dim (5 or 4)
+    ld, rd = (0, 1) if orient == "row" else (1, 0)
     lane = [None] * LANE_BITS
     reg = []
-    # lanes 0..rb-1 -> row bits 0..rb-1
     for i in range(rb):
-        lane[i] = (0, i)
+        lane[i] = (ld, i)
     if MI == 32:
-        # lane bit 5 -> col bit 2 ; regs 0,1 -> col 0,1 ; regs 2,3 -> col 3,4
-        lane[5] = (1, 2)
-        reg += [(1, 0), (1, 1), (1, 3), (1, 4)]
+        # lane bit 5 -> bit 2 of the register dim; regs 0,1 -> bits 0,1; regs 2,3 -> bits 3,4
+        lane[5] = (rd, 2)
+        reg += [(rd, 0), (rd, 1), (rd, 3), (rd, 4)]
     else:
-        # lane bits 4,5 -> col bits 2,3 ; regs 0,1 -> col 0,1
-        lane[4] = (1, 2)
-        lane[5] = (1, 3)
-        reg += [(1, 0), (1, 1)]
+        # lane bits 4,5 -> bits 2,3 of the register dim; regs 0,1 -> bits 0,1
+        lane[4] = (rd, 2)
+        lane[5] = (rd, 3)
+        reg += [(rd, 0), (rd, 1)]
     mb, nb = log2i(M), log2i(N)
     wmb, wnb = log2i(wm), log2i(wn)
     # per-wave repetitions: cols first (adjacent tiles along N), then rows
@@ -325,7 +330,19 @@ def mfma_c(M, N, instr, wm, wn):
     rep_m = list(range(rb, mb - wmb))
     reg += [(1, b) for b in rep_n] + [(0, b) for b in rep_m]
     wave = [(0, b) for b in range(mb - wmb, mb)] + [(1, b) for b in range(nb - wnb, nb)]
-    return Layout((M, N), reg, lane, wave, f"mfma{instr}")
+    return Layout((M, N), reg, lane, wave, f"mfma{instr}" + ("" if orient == "row" else "c"))
+
+
+def mfma_tag_instr(tag):
+    """(instruction, orientation) of an MFMA accumulator layout tag, or None for
+    any other layout (operand fragments, reduction slices, blocked layouts)."""
+    if not tag.startswith("mfma") or tag.startswith("mfmaop") or "/" in tag:
+        return None
+    body = tag[4:]
+    orient = "row"
+    if body.endswith("c"):
+        body, orient = body[:-1], "col"
+    return (body, orient) if body in INSTR else None
 
 
 def mfma_operand(R, K, instr, wr, nwaves_other=1, other_first=False):

@@ -9,16 +9,19 @@ Lowering (this backend's own):
   * instruction: v_mfma_f32_32x32x16_{f16,bf16} when both M and N split into
     32-wide tiles, else 16x16x32 (K % 32 == 0) or 16x16x16; fp32 uses
     v_mfma_f32_32x32x2f32 / 16x16x4f32 (full fp32, no tf32 truncation);
-  * orientation: the MFMA computes C^T = B^T A^T so each lane owns one ROW of
-    the result and the accumulator registers own columns (layouts.mfma_c);
+  * orientation: in kernels that reduce rows (softmax-style statistics of a
+    dot result) the MFMA computes C^T = B^T A^T so each lane owns one ROW of
+    the result and row statistics stay in-lane; elsewhere it computes C = A B
+    directly (layouts.mfma_c);
   * operands are staged into LDS as [rows][K] tiles with K contiguous and
     16-byte chunks XOR-swizzled by row (newt::LdsTile), read back as one
     ds_read_b128 (8 halfs) per lane per MFMA;
-  * B ([K,N], usually N-contiguous in memory) is staged transposed: global
-    loads stay 16-byte vectors along N and the transpose happens on the way
-    into LDS;
-  * inside loops the staging is software-pipelined across iterations (see
-    DotPipeline in ops_pipeline.py).
+  * outside a pipelined loop, B ([K,N], usually N-contiguous in memory) is
+    staged transposed: global loads stay 16-byte vectors along N and the
+    transpose happens on the way into LDS;
+  * k-loops of the plain load/load/dot form are software-pipelined across
+    iterations with direct-to-LDS copies and transposed LDS reads instead
+    (DotPipeline in ops_pipeline.py).
 """
 
 from . import layouts as lo
@@ -79,14 +82,19 @@ class DotOps:
         wm, wn, rep = self.wave_grid(M, N, instr)
         return M, N, K, dt, instr, wm, wn, rep
 
+    def dot_orient(self):
+        """Row-per-lane accumulators when the kernel reduces rows (their row
+        statistics then stay in-lane); plain C = A B orientation otherwise."""
+        return "row" if self.prefer_rows else "col"
+
     def mfma_layout(self, M, N, instr, wm, wn, rep):
-        L = lo.mfma_c(M, N, instr, wm, wn)
+        L = lo.mfma_c(M, N, instr, wm, wn, self.dot_orient())
         if rep > 1:
             L = lo.Layout(L.shape, L.reg, L.lane, list(L.wave) + [None] * lo.log2i(rep), L.tag)
         return L
 
     def init_acc(self, node, acc, Lc, M, N):
-        nacc = lo.INSTR[Lc.tag[4:]][4]
+        nacc = lo.INSTR[lo.mfma_tag_instr(Lc.tag)[0]][4]
         vt = "f32x16" if nacc == 16 else "f32x4"
         out = self.new_reg(tp.float32, (M, N), Lc, vec=nacc)
         nv = Lc.nslots // nacc
@@ -226,8 +234,9 @@ class DotOps:
         self.emit("#pragma unroll")
         self.emit(f"for (int _i = 0; _i < {RM}; ++_i)")
         self.emit("#pragma unroll")
+        x, y = ("_fb[_j]", "_fa[_i]") if self.dot_orient() == "row" else ("_fa[_i]", "_fb[_j]")
         self.emit(f"for (int _j = 0; _j < {RN}; ++_j) {accv.var}[_j + {RN} * _i] = "
-                  f"newt::mfma_{instr}(_fb[_j], _fa[_i], {accv.var}[_j + {RN} * _i]);")
+                  f"newt::mfma_{instr}({x}, {y}, {accv.var}[_j + {RN} * _i]);")
         self.indent -= 1
         self.emit("}")
         self.indent -= 1

@@ -282,7 +282,9 @@ class DotPipeline:
                     self.indent -= 1
                     self.emit("}")
                     continue
-                self.emit(f"if ({cond}) {{")
+                # the in-bounds copy is the hot path; the hint moves the masked
+                # register path out of the loop body's straight-line code
+                self.emit(f"if (__builtin_expect({cond}, 1)) {{")
                 self.indent += 1
                 self._dma_stage(X, base, boff, fmt, R, K, dt)
                 self.indent -= 1
@@ -373,25 +375,24 @@ class DotPipeline:
             self.indent -= 1
             self.emit("}")
 
-    def pipe_mma(self, dstmt, state, acc, slot):
+    def _frag(self, state, which, r0, kk):
         M, N, K, dt, instr = state["M"], state["N"], state["K"], state["dt"], state["instr"]
+        MI = lo.INSTR[instr][0]
+        T = dt.ctype
+        fmt = state["fmt"][which]
+        tile, rows = ("_pa", M) if which == 0 else ("_pb", N)
+        if fmt == "k":
+            return f"newt::lds_frag_k<{T}, {K}, {MI}>({tile}, {r0}, {kk}, _lane)"
+        return f"newt::lds_frag_r<{T}, {rows}, {MI}>({tile}, {r0}, {kk}, _lane)"
+
+    def pipe_frags_first(self, state, slot):
+        """Declare the fragment double buffer of a stage and read k-step 0."""
+        M, N, dt, instr = state["M"], state["N"], state["dt"], state["instr"]
         wm, wn = state["wm"], state["wn"]
-        MI, NI, KI, kpl, nacc = lo.INSTR[instr]
-        Lc = self.mfma_layout(M, N, instr, wm, wn, 1)
-        accv = self.init_acc(dstmt, acc, Lc, M, N)
+        MI, NI = lo.INSTR[instr][:2]
         RM, RN = M // wm // MI, N // wn // NI
         T = dt.ctype
         base = state["names"][slot]
-        fa, fb = state["fmt"]
-
-        def frag(fmt, tile, rows, r0, kk):
-            if fmt == "k":
-                return f"newt::lds_frag_k<{T}, {K}, {MI}>({tile}, {r0}, {kk}, _lane)"
-            return f"newt::lds_frag_r<{T}, {rows}, {MI}>({tile}, {r0}, {kk}, _lane)"
-
-        nks = K // KI
-        self.emit("{")
-        self.indent += 1
         self.emit(f"const {T}* _pa = (const {T}*)({base} + {state['off'][0]});")
         self.emit(f"const {T}* _pb = (const {T}*)({base} + {state['off'][1]});")
         self.emit(f"const int _ra = (_wave & {wm - 1}) * {M // wm};")
@@ -399,10 +400,24 @@ class DotPipeline:
         self.emit(f"i16x8 _fa[2][{RM}], _fb[2][{RN}];")
         self.emit("#pragma unroll")
         self.emit(f"for (int _i = 0; _i < {RM}; ++_i) _fa[0][_i] = "
-                  f"{frag(fa, '_pa', M, f'_ra + _i * {MI}', '0')};")
+                  f"{self._frag(state, 0, f'_ra + _i * {MI}', '0')};")
         self.emit("#pragma unroll")
         self.emit(f"for (int _j = 0; _j < {RN}; ++_j) _fb[0][_j] = "
-                  f"{frag(fb, '_pb', N, f'_rb + _j * {NI}', '0')};")
+                  f"{self._frag(state, 1, f'_rb + _j * {NI}', '0')};")
+
+    def pipe_mma(self, dstmt, state, acc, slot):
+        """MFMAs of one stage, double-buffering fragments across k-steps."""
+        M, N, K, dt, instr = state["M"], state["N"], state["K"], state["dt"], state["instr"]
+        wm, wn = state["wm"], state["wn"]
+        MI, NI, KI, kpl, nacc = lo.INSTR[instr]
+        Lc = self.mfma_layout(M, N, instr, wm, wn, 1)
+        accv = self.init_acc(dstmt, acc, Lc, M, N)
+        RM, RN = M // wm // MI, N // wn // NI
+        T = dt.ctype
+        nks = K // KI
+        self.emit("{")
+        self.indent += 1
+        self.pipe_frags_first(state, slot)
         self.emit("#pragma unroll")
         self.emit(f"for (int _ks = 0; _ks < {nks}; ++_ks) {{")
         self.indent += 1
@@ -410,18 +425,19 @@ class DotPipeline:
         self.indent += 1
         self.emit("#pragma unroll")
         self.emit(f"for (int _i = 0; _i < {RM}; ++_i) _fa[(_ks + 1) & 1][_i] = "
-                  f"{frag(fa, '_pa', M, f'_ra + _i * {MI}', f'(_ks + 1) * {KI}')};")
+                  f"{self._frag(state, 0, f'_ra + _i * {MI}', f'(_ks + 1) * {KI}')};")
         self.emit("#pragma unroll")
         self.emit(f"for (int _j = 0; _j < {RN}; ++_j) _fb[(_ks + 1) & 1][_j] = "
-                  f"{frag(fb, '_pb', N, f'_rb + _j * {NI}', f'(_ks + 1) * {KI}')};")
+                  f"{self._frag(state, 1, f'_rb + _j * {NI}', f'(_ks + 1) * {KI}')};")
         self.indent -= 1
         self.emit("}")
         self.emit("#pragma unroll")
         self.emit(f"for (int _i = 0; _i < {RM}; ++_i)")
         self.emit("#pragma unroll")
+        fa_, fb_ = f"newt::as_frag<{T}>(_fa[_ks & 1][_i])", f"newt::as_frag<{T}>(_fb[_ks & 1][_j])"
+        x, y = (fb_, fa_) if self.dot_orient() == "row" else (fa_, fb_)
         self.emit(f"for (int _j = 0; _j < {RN}; ++_j) {accv.var}[_j + {RN} * _i] = "
-                  f"newt::mfma_{instr}(newt::as_frag<{T}>(_fb[_ks & 1][_j]), "
-                  f"newt::as_frag<{T}>(_fa[_ks & 1][_i]), {accv.var}[_j + {RN} * _i]);")
+                  f"newt::mfma_{instr}({x}, {y}, {accv.var}[_j + {RN} * _i]);")
         self.indent -= 1
         self.emit("}")
         self.indent -= 1
