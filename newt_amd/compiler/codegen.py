@@ -33,7 +33,7 @@ import os
 from . import layouts as lo
 from . import types as tp
 from .values import (Affine, Block, Const, Fill, Lazy, LazyLoad, PtrBlock, Reg, Scalar,
-                     Sym, s_add, s_mul, s_neg)
+                     Staged, Sym, s_add, s_mul, s_neg)
 
 
 class CompileError(Exception):
@@ -149,6 +149,8 @@ class Codegen(ast.NodeVisitor):
         self.dot_state = {}
         self.lds_arrays = []      # (name, bytes): distinct __shared__ arrays (pipeline stages)
         self.pipe_records = []
+        self.pipe_active = None   # pipeline state while its loop body compiles
+        self.pid_remap = False
         self.params = params
         vec = 1
         for _, p in params:
@@ -366,6 +368,8 @@ class Codegen(ast.NodeVisitor):
     def permute(self, v, perm):
         if isinstance(v, (Const, Scalar)):
             return v
+        if isinstance(v, Staged):
+            return Staged(v.rec, v.slot, not v.trans)
         if isinstance(v, LazyLoad):
             ptr = self.permute(v.ptr, perm)
             mask = self.permute(v.mask, perm) if isinstance(v.mask, Block) else v.mask
@@ -572,10 +576,16 @@ class Codegen(ast.NodeVisitor):
     # --------------------------------------------------------- elementwise core
     def pick_layout(self, operands, shape):
         """Layout for an elementwise result: a register operand's layout if one
-        has the full result shape, else one broadcastable into it, else default."""
-        for o in operands:
-            if isinstance(o, Reg) and o.shape == tuple(shape):
+        has the full result shape (preferring layouts that come from an MFMA
+        accumulator, so row statistics and accumulators stay where the matrix
+        cores put them and loop-carried state learns that layout), else one
+        broadcastable into it, else default."""
+        full = [o for o in operands if isinstance(o, Reg) and o.shape == tuple(shape)]
+        for o in full:
+            if o.layout.tag.startswith("mfma") and not o.layout.tag.startswith("mfmaop"):
                 return o.layout
+        if full:
+            return full[0].layout
         for o in operands:
             if isinstance(o, Reg):
                 L = o.layout.broadcast_into(tuple(shape))
@@ -1488,8 +1498,31 @@ class Codegen(ast.NodeVisitor):
         return v.pyval
 
     def op_program_id(self, node, axis):
+        """Program ids are a bijection of the hardware workgroup ids, chosen
+        for MI355X's 8 XCDs: the dispatcher hands consecutive workgroups to
+        XCDs round-robin, so the linear id b is renumbered to
+        (b % 8) * (nb / 8) + b / 8 (for b below the largest multiple of 8) and
+        each XCD runs one contiguous range of programs. Neighbouring programs
+        then share an L2, and a grid whose work varies along axis 0 (causal
+        attention) is spread evenly over the XCDs instead of giving one XCD
+        every eighth, heaviest block. Programs are independent, so any
+        bijection keeps the language's semantics (NEWT_PID_REMAP=0: identity)."""
         ax = self._cx(node, axis, "program_id axis")
-        return self.new_scalar(tp.int32, f"(int)blockIdx.{'xyz'[ax]}")
+        if os.environ.get("NEWT_PID_REMAP", "1") == "0":
+            return self.new_scalar(tp.int32, f"(int)blockIdx.{'xyz'[ax]}")
+        if not self.pid_remap:
+            self.pid_remap = True
+            self.prologue += [
+                "const unsigned _nbx = gridDim.x, _nby = gridDim.y;",
+                "const unsigned _nb = _nbx * _nby * gridDim.z;",
+                "unsigned _pb = blockIdx.x + _nbx * (blockIdx.y + _nby * blockIdx.z);",
+                "{ const unsigned _full = _nb & ~7u;",
+                "  if (_pb < _full) _pb = (_pb & 7u) * (_full >> 3) + (_pb >> 3); }",
+                "const int _pid0 = (int)(_pb % _nbx);",
+                "const int _pid1 = (int)((_pb / _nbx) % _nby);",
+                "const int _pid2 = (int)(_pb / (_nbx * _nby));",
+            ]
+        return Scalar(tp.int32, f"_pid{ax}", Sym(f"_pid{ax}", None, 1))
 
     def op_num_programs(self, node, axis):
         ax = self._cx(node, axis, "num_programs axis")

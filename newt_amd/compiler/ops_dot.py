@@ -26,7 +26,7 @@ Lowering (this backend's own):
 
 from . import layouts as lo
 from . import types as tp
-from .values import Block, Const, Fill, LazyLoad, Reg, Scalar
+from .values import Block, Const, Fill, LazyLoad, Reg, Scalar, Staged
 
 
 def _choose_instr(M, N, K, dt):
@@ -243,11 +243,10 @@ class DotOps:
         self.emit("}")
 
     def op_dot(self, node, a, b, acc=None, out_dtype=None, allow_tf32=None):
+        if isinstance(a, Staged) or isinstance(b, Staged):
+            return self.staged_dot(node, a, b, acc)
         M, N, K, dt, instr, wm, wn, rep = self.dot_geometry(node, a, b)
         Lc = self.mfma_layout(M, N, instr, wm, wn, rep)
-        r = self.pipelined_dot(node, a, b, acc, M, N, K, dt, instr, wm, wn, Lc)
-        if r is not None:
-            return r
         accv = self.init_acc(node, acc, Lc, M, N)
         bA = self.tile_bytes(M, K, dt)
         bB = self.tile_bytes(N, K, dt)
@@ -260,5 +259,3 @@ class DotOps:
         self.emit_mma(accv, instr, M, N, K, wm, wn, area, f"({area} + {bA})", dt)
         return accv
 
-    def pipelined_dot(self, node, a, b, acc, M, N, K, dt, instr, wm, wn, Lc):
-        return None

@@ -1,43 +1,48 @@
-"""Software pipeline for k-loops that feed nl.dot from nl.load.
+"""Software pipeline for loops whose loads feed nl.dot.
 
 The reference stages dot operands through a cp.async ring of `num_stages`
 shared-memory slots with deferred consumption (newt/compiler/codegen.py:
-2279-2369, :2560-2654). This is the gfx950 design of the same idea:
+2279-2369, :2560-2654). This is the gfx950 design of the same idea, for any
+loop whose tiles come from nl.load and go only into nl.dot (the matmul k-loop,
+the K and V tiles of flash attention):
 
-  * the loop is rotated: a prologue issues the operand tiles of the first
-    num_stages-1 iterations, and iteration i issues iteration i+S-1 before it
-    runs the MFMAs of iteration i, so global latency hides behind S-1
-    iterations of matrix work;
-  * every stage is its own __shared__ array, and the main loop is unrolled by
-    S, so each stage is addressed through a distinct LDS object - that lets the
-    compiler see that direct-to-LDS writes into one stage do not alias reads of
-    another and wait for exactly the right loads (s_waitcnt vmcnt(N)) instead
-    of draining everything before each LDS read;
-  * a tile whose rows (or k) are contiguous, 16-byte aligned and proven in
+  * the loop is rotated: a prologue issues the staged tiles of the first
+    num_stages-1 iterations, and iteration i issues those of iteration i+S-1
+    before it computes iteration i, so global latency hides behind S-1
+    iterations of work;
+  * every stage is its own __shared__ array and the main loop is unrolled by S,
+    so each stage is a distinct LDS object - the compiler can see that
+    direct-to-LDS writes into one stage do not alias reads of another and waits
+    for exactly the right loads (s_waitcnt vmcnt(N)) instead of draining all
+    of them before each LDS read;
+  * a tile that is contiguous along one dim, 16-byte aligned and proven in
     bounds by a uniform test is copied global -> LDS with
     global_load_lds_dwordx4 (no VGPR staging, no ds_write); other tiles
     (ragged edges, strided operands) take a register path with the masked
-    loads' `other` fill, written with ds_write;
-  * an operand contiguous along k lands in an XOR-swizzled K-major tile read
-    with ds_read_b128; an operand contiguous along its rows (B of a row-major
-    A @ B) lands R-major and is read with ds_read_b64_tr_b16, so nothing is
-    transposed through registers;
-  * each iteration has one barrier: after it, every wave's copies of the
-    stage to be read are complete and every wave is done reading the stage
-    about to be overwritten.
+    loads' `other` fill, written with ds_write and hinted cold;
+  * a tile is stored with its memory-contiguous dim contiguous in LDS: when
+    that dim is the dot's reduction dim it is an XOR-swizzled K-major tile read
+    with ds_read_b128, otherwise an R-major tile read with ds_read_b64_tr_b16
+    (B of a row-major A @ B, V of attention) - nothing is transposed through
+    registers;
+  * operands that do not change in the loop (attention's Q) are loaded once,
+    before the loop, straight into MFMA operand registers; a dot operand that
+    is the fp16/bf16 cast of another dot's row-per-lane accumulator
+    (attention's P) feeds the MFMA from registers, with the other operand read
+    from LDS in the matching permuted k order;
+  * each iteration has one barrier: after it, every wave's copies of the stage
+    to be read are complete and every wave is done reading the stage about to
+    be overwritten.
 
-Only the plain pattern is pipelined; anything else falls back to synchronous
-staging with identical semantics:
-
-    for k in range(lo, hi, step):          # step a positive constant
-        <assignments: masks, loads ...>    # a = nl.load(...), b = nl.load(...)
-        acc = nl.dot(a, b, acc)
-        <pointer advances: p += ...>
-
-The loaded names, the temporaries and the advanced pointers must not be
-read after the loop (the advances run S-1 iterations ahead), the
-accumulator is read only by the dot, and the body has no stores, atomics or
-nested control flow.
+What is pipelined (else the loop compiles unchanged with synchronous staging):
+a `for k in range(lo, hi, step)` with a positive constant step whose body has
+only assignments (constexpr `if`s are resolved first) and no stores, atomics,
+nested loops or early exits; a staged tile is `x = nl.load(...)` used exactly
+once, as an operand of one nl.dot (directly or through nl.trans / .T), whose
+pointer and mask depend only on the loop variable, loop invariants,
+temporaries computed from those, and pointers advanced by a loop-invariant
+increment after their last use. Advanced pointers and staged names must not be
+read after the loop (the advances run S-1 iterations ahead).
 """
 
 import ast
@@ -45,113 +50,206 @@ import os
 
 from . import layouts as lo
 from . import types as tp
-from .values import Affine, LazyLoad, PtrBlock, Scalar
+from .values import Affine, Const, LazyLoad, Reg, Staged
+
+_SIDE_EFFECTS = {"store", "atomic_add", "atomic_max", "atomic_min"}
 
 
-def _is_call(node, names):
+def _callee(node):
     if not isinstance(node, ast.Call):
-        return False
+        return None
     f = node.func
-    name = f.attr if isinstance(f, ast.Attribute) else getattr(f, "id", None)
-    return name in names
+    return f.attr if isinstance(f, ast.Attribute) else getattr(f, "id", None)
 
 
-_SIDE_EFFECTS = {"store", "atomic_add", "atomic_max", "atomic_min", "static_print", "dot"}
+def _names_read(node):
+    return {n.id for n in ast.walk(node) if isinstance(n, ast.Name) and isinstance(n.ctx, ast.Load)}
+
+
+def _target(s):
+    if isinstance(s, ast.Assign) and len(s.targets) == 1 and isinstance(s.targets[0], ast.Name):
+        return s.targets[0].id
+    if isinstance(s, (ast.AugAssign, ast.AnnAssign)) and isinstance(s.target, ast.Name):
+        return s.target.id
+    return None
+
+
+def _operand_name(a):
+    """(name, transposed) of a dot operand written `x`, `nl.trans(x)` or `x.T`."""
+    trans = False
+    if _callee(a) == "trans" and len(a.args) == 1:
+        a, trans = a.args[0], True
+    elif isinstance(a, ast.Attribute) and a.attr == "T":
+        a, trans = a.value, True
+    return (a.id, trans) if isinstance(a, ast.Name) else (None, trans)
 
 
 class DotPipeline:
     # ------------------------------------------------------------ detection
+    def _const_test(self, test):
+        """Compile-time value of a constexpr `if` test, or None."""
+        if isinstance(test, ast.Constant):
+            return bool(test.value)
+        if isinstance(test, ast.Name):
+            v = self.locals.get(test.id)
+            if isinstance(v, Const) and test.id not in self.storages:
+                return bool(v.pyval)
+            return None
+        if isinstance(test, ast.UnaryOp) and isinstance(test.op, ast.Not):
+            v = self._const_test(test.operand)
+            return None if v is None else not v
+        return None
+
+    def _flatten(self, stmts):
+        out = []
+        for s in stmts:
+            if isinstance(s, ast.If):
+                v = self._const_test(s.test)
+                if v is None:
+                    return None
+                sub = self._flatten(s.body if v else s.orelse)
+                if sub is None:
+                    return None
+                out += sub
+            elif isinstance(s, (ast.Assign, ast.AugAssign, ast.AnnAssign)):
+                if _target(s) is None or getattr(s, "value", None) is None:
+                    return None
+                out.append(s)
+            elif isinstance(s, ast.Pass):
+                continue
+            else:
+                return None
+        return out
+
     def pipeline_plan(self, node):
         if self.num_stages < 2 or os.environ.get("NEWT_PIPELINE_DOT", "1") == "0":
             return None
         if self.hints.get(("nopipe", node.lineno)):
             return None
-        body = node.body
-        dots = [i for i, s in enumerate(body)
-                if isinstance(s, ast.Assign) and _is_call(s.value, {"dot"})]
-        if len(dots) != 1:
-            return None
-        di = dots[0]
-        dstmt = body[di]
-        if len(dstmt.targets) != 1 or not isinstance(dstmt.targets[0], ast.Name):
-            return None
-        accn = dstmt.targets[0].id
-        call = dstmt.value
-        args = list(call.args)
-        kw = {k.arg: k.value for k in call.keywords}
-        if len(args) == 2 and "acc" in kw:
-            args.append(kw.pop("acc"))
-        if len(args) != 3 or kw or not all(isinstance(x, ast.Name) for x in args):
-            return None
-        an, bn, cn = (x.id for x in args)
-        if cn != accn or len({an, bn, accn}) != 3:
-            return None
-        pre, post = body[:di], body[di + 1:]
-        temps = set()
-        loads = set()
-        for s in pre:
-            if not (isinstance(s, ast.Assign) and len(s.targets) == 1
-                    and isinstance(s.targets[0], ast.Name)):
-                return None
-            if any(_is_call(n, _SIDE_EFFECTS) for n in ast.walk(s)):
-                return None
-            temps.add(s.targets[0].id)
-            if _is_call(s.value, {"load"}):
-                loads.add(s.targets[0].id)
-        if an not in loads or bn not in loads:
-            return None
-        carried = set()
-        for s in post:
-            if isinstance(s, ast.AugAssign) and isinstance(s.target, ast.Name):
-                carried.add(s.target.id)
-            elif (isinstance(s, ast.Assign) and len(s.targets) == 1
-                  and isinstance(s.targets[0], ast.Name)):
-                carried.add(s.targets[0].id)
-            else:
-                return None
-            if any(_is_call(n, _SIDE_EFFECTS) for n in ast.walk(s)):
-                return None
-        reads_post = {n.id for s in post for n in ast.walk(s) if isinstance(n, ast.Name)
-                      and isinstance(n.ctx, ast.Load)}
-        if reads_post & (temps | {accn}):
-            return None
-        reads_pre = {n.id for s in pre for n in ast.walk(s) if isinstance(n, ast.Name)
-                     and isinstance(n.ctx, ast.Load)}
-        if accn in reads_pre or (temps & carried) or accn in temps | carried:
-            return None
-        # a and b are read by the dot only
-        uses = [n.id for s in pre for n in ast.walk(s) if isinstance(n, ast.Name)
-                and isinstance(n.ctx, ast.Load)]
-        if an in uses or bn in uses:
+        flat = self._flatten(node.body)
+        if not flat:
             return None
         kname = node.target.id
-        if any(t in self.locals or t in self.storages for t in temps | {kname}):
+        for s in flat:
+            if any(_callee(n) in _SIDE_EFFECTS for n in ast.walk(s)):
+                return None
+        assigned = {}
+        for i, s in enumerate(flat):
+            assigned.setdefault(_target(s), []).append(i)
+        if kname in assigned:
             return None
-        if not all(c in self.locals or c in self.storages for c in carried):
+        uses = {}
+        for s in flat:
+            for n in ast.walk(s):
+                if _callee(n) != "dot":
+                    continue
+                for role, a in zip(("A", "B"), list(n.args)[:2]):
+                    nm, trans = _operand_name(a)
+                    if nm is not None:
+                        uses.setdefault(nm, []).append((role, trans))
+        reads = {}
+        for s in flat:
+            for n in ast.walk(s):
+                if isinstance(n, ast.Name) and isinstance(n.ctx, ast.Load):
+                    reads[n.id] = reads.get(n.id, 0) + 1
+
+        def invariant(nm):
+            return nm not in assigned and nm != kname
+
+        # pointers advanced by a loop-invariant increment after their last read
+        carried = set()
+        for nm, idx in assigned.items():
+            if len(idx) != 1 or not isinstance(flat[idx[0]], ast.AugAssign):
+                continue
+            s = flat[idx[0]]
+            if not all(invariant(r) for r in _names_read(s.value)):
+                continue
+            if any(nm in _names_read(t) for t in flat[idx[0] + 1:]):
+                continue
+            if nm in self.locals or nm in self.storages:
+                carried.add(nm)
+        # temporaries that are pure functions of the loop variable and invariants
+        konly = set()
+        for s in flat:
+            nm = _target(s)
+            if nm in carried or len(assigned[nm]) != 1 or not isinstance(s, ast.Assign):
+                continue
+            if any(_callee(n) in ("load", "dot") for n in ast.walk(s.value)):
+                continue
+            if all(r == kname or invariant(r) or r in konly or r in carried
+                   for r in _names_read(s.value)):
+                konly.add(nm)
+        staged = {}
+        for i, s in enumerate(flat):
+            nm = _target(s)
+            if not (isinstance(s, ast.Assign) and _callee(s.value) == "load"):
+                continue
+            if len(assigned[nm]) != 1 or len(uses.get(nm, [])) != 1 or reads.get(nm) != 1:
+                continue
+            if nm in self.locals or nm in self.storages:
+                continue
+            if not all(r == kname or invariant(r) or r in konly or r in carried
+                       for r in _names_read(s.value)):
+                continue
+            role, trans = uses[nm][0]
+            # reduction dim of the tile as loaded: A [M,K] -> 1, B [K,N] -> 0
+            kdim = (1 if role == "A" else 0) ^ (1 if trans else 0)
+            staged[nm] = {"name": nm, "index": i, "kdim": kdim}
+        if not staged:
             return None
-        if (temps | carried | {kname}) & self._read_after():
+        # the statements computing the staged tiles' pointers and masks
+        need = set()
+        for rec in staged.values():
+            need |= _names_read(flat[rec["index"]].value)
+        slice_idx = set(rec["index"] for rec in staged.values())
+        changed = True
+        while changed:
+            changed = False
+            for i, s in enumerate(flat):
+                nm = _target(s)
+                if nm in konly and nm in need and i not in slice_idx:
+                    slice_idx.add(i)
+                    need |= _names_read(s.value)
+                    changed = True
+        # advanced pointers may only be read by the slice
+        for nm in sorted(carried):
+            readers = [i for i, s in enumerate(flat) if nm in _names_read(s)
+                       and i != assigned[nm][0]]
+            if any(i not in slice_idx for i in readers):
+                return None
+        if (carried | set(staged)) & self._read_after():
             return None
-        return pre, dstmt, post, an, bn, accn, temps
+        # temporaries of the loop are recomputed each iteration, so they must
+        # not be defined before it
+        if any(t in self.locals or t in self.storages for t in konly):
+            return None
+        return {"flat": flat, "staged": staged, "slice": sorted(slice_idx),
+                "advance": sorted(assigned[nm][0] for nm in carried), "konly": konly,
+                "kname": kname, "node": node}
 
     # ----------------------------------------------------------- emission
     def pipelined_for(self, node, plan, lo_, hi, st, idt):
-        pre, dstmt, post, an, bn, accn, temps = plan
         S = int(self.hints.get(("pipe_stages", node.lineno), self.num_stages))
-        kname = node.target.id
+        flat, staged, kname = plan["flat"], plan["staged"], plan["kname"]
+        slice_stmts = [flat[i] for i in plan["slice"]]
+        advance = [flat[i] for i in plan["advance"]]
+        skip = set(plan["advance"]) | set(rec["index"] for rec in staged.values())
+        temps = plan["konly"] | set(staged) | {kname}
         stv = int(st.pyval)
         lo_e = self.scalar_expr(lo_, idt)
         hi_e = self.scalar_expr(hi, idt)
         n = self.new_scalar(idt, f"((({hi_e}) > ({lo_e})) ? ((({hi_e}) - ({lo_e}) + {stv - 1}) "
                                  f"/ {stv}) : 0)")
-        state = {"node": node, "S": S, "dot": dstmt.value}
+        state = {"node": node, "S": S, "recs": None, "plan": plan}
         self.pipe_records.append(state)
         for s in range(S - 1):
             self.locals[kname] = self.new_scalar(idt, f"({lo_e} + {s * stv})")
-            self.visit_body(pre)
-            self.pipe_issue(state, an, bn, s, f"({s} < {n.expr})")
-            self.visit_body(post)
-            for t in temps | {kname}:
+            self.visit_body(slice_stmts)
+            self.pipe_issue(state, s, f"({s} < {n.expr})")
+            self.visit_body(advance)
+            for t in temps:
                 self.locals.pop(t, None)
+        self.pipe_hoist_operands(state)
         rec = self._enter_compound(node)
         self.drain_dots_for_loop(node)
         it0 = self.fresh("it")
@@ -159,6 +257,7 @@ class DotPipeline:
         self.indent += 1
         self.loop_depth += 1
         ops = state["ops"]
+        self.pipe_active = state
         for s in range(S):
             it = f"({it0} + {s})"
             if s:
@@ -171,14 +270,21 @@ class DotPipeline:
                 self.emit("newt::wait_vmcnt<0>();")
             self.emit("__syncthreads();")
             self.emit("__builtin_amdgcn_sched_barrier(0);")
+            # issue iteration it+S-1 into the stage that iteration it-1 read
             self.locals[kname] = self.new_scalar(idt, f"({lo_e} + ({it} + {S - 1}) * {stv})")
-            self.visit_body(pre)
-            self.pipe_issue(state, an, bn, (s + S - 1) % S, f"({it} + {S - 1} < {n.expr})")
-            self.visit_body(post)
-            for t in temps | {kname}:
+            self.visit_body(slice_stmts)
+            self.pipe_issue(state, (s + S - 1) % S, f"({it} + {S - 1} < {n.expr})")
+            self.visit_body(advance)
+            for t in temps:
                 self.locals.pop(t, None)
-            acc = self.lookup(dstmt, accn)
-            self.bind(dstmt, accn, self.pipe_mma(dstmt, state, acc, s))
+            # compute iteration it from stage s
+            self.locals[kname] = self.new_scalar(idt, f"({lo_e} + {it} * {stv})")
+            for nm, r in state["recs"].items():
+                self.locals[nm] = Staged(r, s)
+            self.visit_body([x for i, x in enumerate(flat) if i not in skip])
+            for t in temps:
+                self.locals.pop(t, None)
+        self.pipe_active = None
         self.flush_loads()
         self.loop_backedge(node)
         self.loop_depth -= 1
@@ -192,11 +298,16 @@ class DotPipeline:
         from .codegen import _Retry
         raise _Retry()
 
-    def _tile_format(self, X, R, K):
-        """'k' (K contiguous, ds_read_b128) or 'r' (rows contiguous, tr16 reads)."""
+    # --------------------------------------------------------------- staging
+    def _tile_format(self, X, kdim):
+        """LDS format of a staged tile: 'k' when its unit-stride dim is the
+        reduction dim (or neither dim is unit-stride), 'r' when it is the row
+        dim."""
         off = X.ptr.offset
+        R = X.shape[1 - kdim]
+        K = X.shape[kdim]
         if isinstance(off, Affine):
-            ck, cr = off.coefs.get(1), off.coefs.get(0)
+            ck, cr = off.coefs.get(kdim), off.coefs.get(1 - kdim)
             if ck is not None and ck.is_const and ck.const == 1 and K % 8 == 0:
                 return "k"
             if cr is not None and cr.is_const and cr.const == 1 and R % 32 == 0:
@@ -204,7 +315,8 @@ class DotPipeline:
         return "k"
 
     def _dma_ok(self, X, fmt, R, K, dt):
-        """Compile-time conditions for global_load_lds of whole 16-byte chunks."""
+        """Compile-time conditions for global_load_lds of whole 16-byte chunks
+        (X is the [R, K] view)."""
         off = X.ptr.offset
         if not isinstance(off, Affine) or not X.ptr.base.aligned16:
             return False
@@ -219,93 +331,87 @@ class DotPipeline:
             return False
         if off.base.div % epc:
             return False
-        chunks = R * K // epc
-        return chunks % self.T == 0
+        return (R * K // epc) % self.T == 0
 
-    def pipe_geometry(self, state, a, b):
-        dnode = state["dot"]
-        M, N, K, dt, instr, wm, wn, rep = self.dot_geometry(dnode, a, b)
-        MI, NI, KI, kpl, nacc = lo.INSTR[instr]
-        if rep > 1 or dt not in (tp.float16, tp.bfloat16) or kpl != 8:
-            self._no_pipe(state)
-        Bt = self.permute(b, (1, 0))
-        fa = self._tile_format(a, M, K)
-        fb = self._tile_format(Bt, N, K)
-        ba = self.tile_bytes(M, K, dt)
-        bb = self.tile_bytes(N, K, dt)
-        stage = (ba + bb + 15) // 16 * 16
-        names = []
-        for j in range(state["S"]):
-            nm = f"_ldsP{len(self.lds_arrays)}"
-            self.lds_arrays.append((nm, stage))
-            names.append(nm)
-        dma_a = self._dma_ok(a, fa, M, K, dt)
-        dma_b = self._dma_ok(Bt, fb, N, K, dt)
-        epc = 16 // dt.itemsize
-        ops = (M * K // epc // self.T if dma_a else 0) + (N * K // epc // self.T if dma_b else 0)
-        state.update(M=M, N=N, K=K, dt=dt, instr=instr, wm=wm, wn=wn, fmt=(fa, fb),
-                     off=(0, ba), names=names, dma=(dma_a, dma_b), ops=ops)
-        return Bt
-
-    def pipe_issue(self, state, an, bn, slot, valid):
-        a, b = self.locals.get(an), self.locals.get(bn)
-        if not isinstance(a, LazyLoad) or not isinstance(b, LazyLoad) or a.result is not None \
-                or b.result is not None:
-            self._no_pipe(state)
-        if "M" not in state:
-            Bt = self.pipe_geometry(state, a, b)
-        else:
-            if (a.shape, b.shape, a.dtype) != ((state["M"], state["K"]), (state["K"], state["N"]),
-                                              state["dt"]):
+    def _init_recs(self, state):
+        recs = {}
+        off = 0
+        ops = 0
+        for nm, info in sorted(state["plan"]["staged"].items(), key=lambda kv: kv[1]["index"]):
+            X = self.locals.get(nm)
+            if not isinstance(X, LazyLoad) or X.result is not None or len(X.shape) != 2:
                 self._no_pipe(state)
-            Bt = self.permute(b, (1, 0))
-        dt = state["dt"]
-        T = dt.ctype
-        ops = [(a, state["M"], state["fmt"][0], state["off"][0], state["dma"][0], a),
-               (Bt, state["N"], state["fmt"][1], state["off"][1], state["dma"][1], b)]
-        # register-path operands first: their (synchronous) loads must not
-        # drain the asynchronous copies issued for this stage
-        ops.sort(key=lambda o: o[4])
-        K = state["K"]
+            dt = X.dtype
+            if dt not in (tp.float16, tp.bfloat16):
+                self._no_pipe(state)
+            kdim = info["kdim"]
+            V = X if kdim == 1 else self.permute(X, (1, 0))   # [R, K] view
+            R, K = V.shape
+            if K % 16 or R % 16:
+                self._no_pipe(state)
+            fmt = self._tile_format(X, kdim)
+            nbytes = self.tile_bytes(R, K, dt)
+            dma = self._dma_ok(V, fmt, R, K, dt)
+            epc = 16 // dt.itemsize
+            if dma:
+                ops += R * K // epc // self.T
+            recs[nm] = {"name": nm, "shape": tuple(X.shape), "dt": dt, "kdim": kdim, "R": R,
+                        "K": K, "fmt": fmt, "off": off, "dma": dma}
+            off += (nbytes + 15) // 16 * 16
+            if V is not X:
+                V.consumed = True
+                if V in self.pending_loads:
+                    self.pending_loads.remove(V)
+        names = []
+        for _ in range(state["S"]):
+            nm = f"_ldsP{len(self.lds_arrays)}"
+            self.lds_arrays.append((nm, off))
+            names.append(nm)
+        state.update(recs=recs, ops=ops, names=names)
+
+    def pipe_issue(self, state, slot, valid):
+        if state["recs"] is None:
+            self._init_recs(state)
         base = state["names"][slot]
+        # register-path tiles first: their (synchronous) loads must not drain
+        # the asynchronous copies issued for this stage
+        order = sorted(state["recs"].values(), key=lambda r: (r["dma"], r["off"]))
         self.emit("{")
         self.indent += 1
-        for X, R, fmt, boff, dma, src in ops:
-            tile = f"(({T}*)({base} + {boff}))"
-            if dma:
-                full = self.mask_all_true(src.mask, src.shape)
-                cond = valid if full in (None, "true") else f"{valid} && ({full})"
-                if full is None:
-                    self.emit(f"if ({valid}) {{")
-                    self.indent += 1
-                    self._reg_stage(X, tile, fmt, R, K, dt)
-                    self.indent -= 1
-                    self.emit("}")
-                    continue
+        for r in order:
+            X = self.locals.get(r["name"])
+            if not isinstance(X, LazyLoad) or X.result is not None or tuple(X.shape) != r["shape"]:
+                self._no_pipe(state)
+            V = X if r["kdim"] == 1 else self.permute(X, (1, 0))
+            dt, R, K, fmt = r["dt"], r["R"], r["K"], r["fmt"]
+            tile = f"(({dt.ctype}*)({base} + {r['off']}))"
+            full = self.mask_all_true(X.mask, X.shape) if r["dma"] else None
+            if r["dma"] and full is not None:
+                cond = valid if full == "true" else f"{valid} && ({full})"
                 # the in-bounds copy is the hot path; the hint moves the masked
-                # register path out of the loop body's straight-line code
+                # register path out of the loop's straight-line code
                 self.emit(f"if (__builtin_expect({cond}, 1)) {{")
                 self.indent += 1
-                self._dma_stage(X, base, boff, fmt, R, K, dt)
+                self._dma_stage(V, base, r["off"], fmt, R, K, dt)
                 self.indent -= 1
                 if full != "true":
                     self.emit(f"}} else if ({valid}) {{")
                     self.indent += 1
-                    self._reg_stage(X, tile, fmt, R, K, dt)
+                    self._reg_stage(V, tile, fmt, R, K, dt)
                     self.indent -= 1
                 self.emit("}")
             else:
                 self.emit(f"if ({valid}) {{")
                 self.indent += 1
-                self._reg_stage(X, tile, fmt, R, K, dt)
+                self._reg_stage(V, tile, fmt, R, K, dt)
                 self.indent -= 1
                 self.emit("}")
+            for ld in (X, V):
+                ld.consumed = True
+                if ld in self.pending_loads:
+                    self.pending_loads.remove(ld)
         self.indent -= 1
         self.emit("}")
-        for ld in (a, b, Bt):
-            ld.consumed = True
-            if ld in self.pending_loads:
-                self.pending_loads.remove(ld)
 
     def _dma_stage(self, X, base, boff, fmt, R, K, dt):
         off = X.ptr.offset
@@ -375,71 +481,163 @@ class DotPipeline:
             self.indent -= 1
             self.emit("}")
 
-    def _frag(self, state, which, r0, kk):
-        M, N, K, dt, instr = state["M"], state["N"], state["K"], state["dt"], state["instr"]
-        MI = lo.INSTR[instr][0]
-        T = dt.ctype
-        fmt = state["fmt"][which]
-        tile, rows = ("_pa", M) if which == 0 else ("_pb", N)
-        if fmt == "k":
-            return f"newt::lds_frag_k<{T}, {K}, {MI}>({tile}, {r0}, {kk}, _lane)"
-        return f"newt::lds_frag_r<{T}, {rows}, {MI}>({tile}, {r0}, {kk}, _lane)"
+    # ------------------------------------------------- loop-invariant operands
+    def _dot_operand_shape(self, a, state):
+        """(shape, name) of a dot operand expression, without emitting code;
+        name is None for transposed or non-name operands."""
+        nm, trans = _operand_name(a)
+        if nm is None:
+            return None, None
+        if nm in state["recs"]:
+            sh = state["recs"][nm]["shape"]
+        else:
+            sh = getattr(self.locals.get(nm), "shape", None)
+            if sh is None or len(sh) != 2:
+                return None, None
+        sh = tuple(sh)
+        return (sh[::-1] if trans else sh), (None if trans else nm)
 
-    def pipe_frags_first(self, state, slot):
-        """Declare the fragment double buffer of a stage and read k-step 0."""
-        M, N, dt, instr = state["M"], state["N"], state["dt"], state["instr"]
-        wm, wn = state["wm"], state["wn"]
-        MI, NI = lo.INSTR[instr][:2]
-        RM, RN = M // wm // MI, N // wn // NI
-        T = dt.ctype
-        base = state["names"][slot]
-        self.emit(f"const {T}* _pa = (const {T}*)({base} + {state['off'][0]});")
-        self.emit(f"const {T}* _pb = (const {T}*)({base} + {state['off'][1]});")
-        self.emit(f"const int _ra = (_wave & {wm - 1}) * {M // wm};")
-        self.emit(f"const int _rb = ((_wave >> {lo.log2i(wm)}) & {wn - 1}) * {N // wn};")
-        self.emit(f"i16x8 _fa[2][{RM}], _fb[2][{RN}];")
-        self.emit("#pragma unroll")
-        self.emit(f"for (int _i = 0; _i < {RM}; ++_i) _fa[0][_i] = "
-                  f"{self._frag(state, 0, f'_ra + _i * {MI}', '0')};")
-        self.emit("#pragma unroll")
-        self.emit(f"for (int _j = 0; _j < {RN}; ++_j) _fb[0][_j] = "
-                  f"{self._frag(state, 1, f'_rb + _j * {NI}', '0')};")
+    def pipe_hoist_operands(self, state):
+        """Load A operands that do not change in the loop into MFMA operand
+        registers once, before it."""
+        plan = state["plan"]
+        assigned = {_target(s) for s in plan["flat"]}
+        for s in plan["flat"]:
+            for nd in ast.walk(s):
+                if _callee(nd) != "dot" or len(nd.args) < 2:
+                    continue
+                sa, na = self._dot_operand_shape(nd.args[0], state)
+                sb, _ = self._dot_operand_shape(nd.args[1], state)
+                if sa is None or sb is None or sa[1] != sb[0]:
+                    continue
+                if na is None or na in assigned or na in state["recs"] or na in self.storages:
+                    continue
+                v = self.locals.get(na)
+                if not isinstance(v, (LazyLoad, Reg)) or v.dtype not in (tp.float16, tp.bfloat16):
+                    continue
+                geo = self._geometry_of(sa[0], sb[1], sa[1], v.dtype)
+                if geo is None:
+                    continue
+                instr, wm, wn = geo
+                L = lo.mfma_operand(sa[0], sa[1], instr, wm, wn, other_first=False)
+                if isinstance(v, Reg) and v.layout == L:
+                    continue
+                self.locals[na] = self.to_reg(v, L)
 
-    def pipe_mma(self, dstmt, state, acc, slot):
-        """MFMAs of one stage, double-buffering fragments across k-steps."""
-        M, N, K, dt, instr = state["M"], state["N"], state["K"], state["dt"], state["instr"]
-        wm, wn = state["wm"], state["wn"]
+    def _geometry_of(self, M, N, K, dt):
+        from .ops_dot import _choose_instr
+        if M % 16 or N % 16 or K % 16 or M < 16 or N < 16:
+            return None
+        instr = _choose_instr(M, N, K, dt)
+        if lo.INSTR[instr][3] != 8:
+            return None
+        wm, wn, rep = self.wave_grid(M, N, instr)
+        if rep > 1:
+            return None
+        return instr, wm, wn
+
+    # ------------------------------------------------------------- the dot
+    @staticmethod
+    def _slot_for(L, coords):
+        """Register slot of L that holds the element whose in-thread
+        coordinate parts are `coords` (dim -> value, lane/wave parts excluded)."""
+        s = 0
+        want = dict(coords)
+        for i, b in enumerate(L.reg):
+            if b is None:
+                continue
+            d, bit = b
+            if (want.get(d, 0) >> bit) & 1:
+                s |= 1 << i
+                want[d] = want[d] & ~(1 << bit)
+        if any(want.values()):
+            raise ValueError("coordinate not held in registers")
+        return s
+
+    def staged_dot(self, node, a, b, acc):
+        """nl.dot with at least one operand resident in a pipeline stage."""
+        M, N, K, dt, instr, wm, wn, rep = self.dot_geometry(node, a, b)
         MI, NI, KI, kpl, nacc = lo.INSTR[instr]
+        state = getattr(self, "pipe_active", None)
+        if rep > 1 or kpl != 8 or dt not in (tp.float16, tp.bfloat16) or state is None:
+            if state is not None:
+                self._no_pipe(state)
+            self.err(node, "internal: staged operand in an unsupported dot")
         Lc = self.mfma_layout(M, N, instr, wm, wn, 1)
-        accv = self.init_acc(dstmt, acc, Lc, M, N)
-        RM, RN = M // wm // MI, N // wn // NI
         T = dt.ctype
+        Bt = Staged(b.rec, b.slot, not b.trans) if isinstance(b, Staged) else self.permute(b, (1, 0))
+        RM, RN = M // wm // MI, N // wn // NI
         nks = K // KI
+        orient = self.dot_orient()
+        # an accumulator-layout A operand (fp16/bf16 cast of a row-per-lane dot
+        # result) is used in place, with B read in the permuted k order
+        perm = (orient == "row" and MI == 32 and isinstance(a, Reg) and isinstance(Bt, Staged)
+                and wn == 1 and a.layout == lo.mfma_c(M, K, instr, wm, 1, "row"))
+        srcs = []
+        for role, X in (("A", a), ("B", Bt)):
+            if isinstance(X, Staged):
+                srcs.append(("lds", X))
+            elif role == "A" and perm:
+                srcs.append(("acc", X))
+            else:
+                if role == "A":
+                    L = lo.mfma_operand(M, K, instr, wm, wn, other_first=False)
+                else:
+                    L = lo.mfma_operand(N, K, instr, wn, wm, other_first=True)
+                r = X if isinstance(X, Reg) and X.layout == L and not X.vec else self.to_reg(X, L)
+                if r.dtype != dt:
+                    r = self.to_reg(r, r.layout, dt)
+                srcs.append(("op", r))
+        accv = self.init_acc(node, acc, Lc, M, N)
         self.emit("{")
         self.indent += 1
-        self.pipe_frags_first(state, slot)
-        self.emit("#pragma unroll")
-        self.emit(f"for (int _ks = 0; _ks < {nks}; ++_ks) {{")
-        self.indent += 1
-        self.emit(f"if (_ks + 1 < {nks}) {{")
-        self.indent += 1
-        self.emit("#pragma unroll")
-        self.emit(f"for (int _i = 0; _i < {RM}; ++_i) _fa[(_ks + 1) & 1][_i] = "
-                  f"{self._frag(state, 0, f'_ra + _i * {MI}', f'(_ks + 1) * {KI}')};")
-        self.emit("#pragma unroll")
-        self.emit(f"for (int _j = 0; _j < {RN}; ++_j) _fb[(_ks + 1) & 1][_j] = "
-                  f"{self._frag(state, 1, f'_rb + _j * {NI}', f'(_ks + 1) * {KI}')};")
-        self.indent -= 1
-        self.emit("}")
-        self.emit("#pragma unroll")
-        self.emit(f"for (int _i = 0; _i < {RM}; ++_i)")
-        self.emit("#pragma unroll")
-        fa_, fb_ = f"newt::as_frag<{T}>(_fa[_ks & 1][_i])", f"newt::as_frag<{T}>(_fb[_ks & 1][_j])"
-        x, y = (fb_, fa_) if self.dot_orient() == "row" else (fa_, fb_)
-        self.emit(f"for (int _j = 0; _j < {RN}; ++_j) {accv.var}[_j + {RN} * _i] = "
-                  f"newt::mfma_{instr}({x}, {y}, {accv.var}[_j + {RN} * _i]);")
-        self.indent -= 1
-        self.emit("}")
+        self.emit(f"const int _ra = (_wave & {wm - 1}) * {M // wm};")
+        self.emit(f"const int _rb = ((_wave >> {lo.log2i(wm)}) & {wn - 1}) * {N // wn};")
+        tiles = {}
+        for idx, (kind, X) in enumerate(srcs):
+            if kind == "lds":
+                nm = f"_pt{idx}"
+                self.emit(f"const {T}* {nm} = (const {T}*)({state['names'][X.slot]} + "
+                          f"{X.rec['off']});")
+                tiles[idx] = nm
+
+        def frag(idx, i, ks):
+            kind, X = srcs[idx]
+            kk = ks * KI
+            if kind == "lds":
+                rec, tile = X.rec, tiles[idx]
+                r0 = f"{'_ra' if idx == 0 else '_rb'} + {i * MI}"
+                if rec["fmt"] == "k":
+                    fn, targs = (("lds_frag_k_perm32", f"{T}, {rec['K']}") if perm else
+                                 ("lds_frag_k", f"{T}, {rec['K']}, {MI}"))
+                else:
+                    fn, targs = (("lds_frag_r_perm32", f"{T}, {rec['R']}") if perm else
+                                 ("lds_frag_r", f"{T}, {rec['R']}, {MI}"))
+                return f"newt::{fn}<{targs}>({tile}, {r0}, {kk}, _lane)"
+            if kind == "acc":
+                slots = [self._slot_for(X.layout, {0: i * MI, 1: kk + 8 * (e // 4) + (e % 4)})
+                         for e in range(8)]
+            else:
+                slots = [self._slot_for(X.layout, {0: i * MI, 1: kk + e}) for e in range(8)]
+            return f"newt::pack8<{T}>({', '.join(X.at(s) for s in slots)})"
+
+        def emit_frags(ks):
+            for i in range(RM):
+                self.emit(f"const i16x8 _fa{ks}_{i} = {frag(0, i, ks)};")
+            for j in range(RN):
+                self.emit(f"const i16x8 _fb{ks}_{j} = {frag(1, j, ks)};")
+
+        emit_frags(0)
+        for ks in range(nks):
+            if ks + 1 < nks:
+                emit_frags(ks + 1)
+            for i in range(RM):
+                for j in range(RN):
+                    fa_ = f"newt::as_frag<{T}>(_fa{ks}_{i})"
+                    fb_ = f"newt::as_frag<{T}>(_fb{ks}_{j})"
+                    x, y = (fb_, fa_) if orient == "row" else (fa_, fb_)
+                    v = f"{accv.var}[{j + RN * i}]"
+                    self.emit(f"{v} = newt::mfma_{instr}({x}, {y}, {v});")
         self.indent -= 1
         self.emit("}")
         return accv

@@ -235,3 +235,22 @@ class Reg(Block):
 
     def __repr__(self):
         return f"Reg({self.dtype}, {self.shape}, {self.var}, {self.layout.tag})"
+
+
+class Staged(Block):
+    """A dot operand tile resident in one LDS stage of a pipelined loop.
+
+    rec is the staged load's record (shape and dtype as loaded, LDS format,
+    byte offset inside the stage); slot the stage index; trans a transposed
+    view (nl.trans of the loaded block). Only nl.dot consumes these."""
+
+    def __init__(self, rec, slot, trans=False):
+        self.rec = rec
+        self.slot = slot
+        self.trans = trans
+        self.dtype = rec["dt"]
+        r0, r1 = rec["shape"]
+        self.shape = (r1, r0) if trans else (r0, r1)
+
+    def __repr__(self):
+        return f"Staged({self.rec['name']}, slot={self.slot}, trans={self.trans})"

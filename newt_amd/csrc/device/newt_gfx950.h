@@ -308,6 +308,24 @@ __device__ __forceinline__ i16x8 lds_frag_r(const T* tile, int r0, int kk, int l
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Same fragment with the k order permuted the way a 32x32 MFMA accumulator
+// holds its columns (lane half h owns columns 4h..4h+3 and 8+4h..8+4h+3 of
+// each 16): element e of lane half h is k = kk + 8*(e/4) + 4h + e%4. A
+// probability tile produced by one MFMA can then feed the next one straight
+// from registers, with the other operand read in the matching order.
+template <typename T, int RD>
+__device__ __forceinline__ i16x8 lds_frag_r_perm32(const T* tile, int r0, int kk, int lane) {
+  typedef LdsTileR<T, RD> L;
+  const int i = lane & 15;
+  const int cb = r0 + (lane & 16) + 4 * (i & 3);
+  const int kr = kk + 4 * (lane >> 5) + (i >> 2);
+  const __attribute__((address_space(3))) char* b =
+      (const __attribute__((address_space(3))) char*)tile;
+  i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(b + 2 * L::off(kr, cb)));
+  i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(b + 2 * L::off(kr + 8, cb)));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // Fragment of a K-major tile (LdsTile): lane l gets row r0 + (l % MI) and
 // k = kk + 8 * (l / MI) + 0..7 as one ds_read_b128.
 template <typename T, int KD, int MI>
@@ -338,6 +356,25 @@ template <> struct frag8<bf16> { typedef bf16x8 type; };
 template <typename T>
 __device__ __forceinline__ typename frag8<T>::type as_frag(i16x8 v) {
   return __builtin_bit_cast(typename frag8<T>::type, v);
+}
+
+// K-major tile fragment in the permuted 32x32 accumulator k order (see
+// lds_frag_r_perm32): two 8-byte reads per lane.
+template <typename T, int KD>
+__device__ __forceinline__ i16x8 lds_frag_k_perm32(const T* tile, int r0, int kk, int lane) {
+  typedef LdsTile<T, KD> L;
+  const int r = r0 + (lane & 31);
+  const int k = kk + 4 * (lane >> 5);
+  i16x4 lo = *(const i16x4*)(tile + L::off(r, k));
+  i16x4 hi = *(const i16x4*)(tile + L::off(r, k + 8));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Eight 16-bit register values as one MFMA operand fragment.
+template <typename T>
+__device__ __forceinline__ i16x8 pack8(T a0, T a1, T a2, T a3, T a4, T a5, T a6, T a7) {
+  typename frag8<T>::type v = {a0, a1, a2, a3, a4, a5, a6, a7};
+  return __builtin_bit_cast(i16x8, v);
 }
 
 }  // namespace newt

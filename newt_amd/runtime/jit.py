@@ -221,7 +221,8 @@ class JITFunction:
     @staticmethod
     def _key(constexprs, types, num_warps, num_stages):
         env = tuple(os.environ.get(k, "") for k in ("NEWT_VEC", "NEWT_PIPELINE_DOT",
-                                                    "NEWT_LDS_DMA", "NEWT_MFMA"))
+                                                    "NEWT_LDS_DMA", "NEWT_MFMA",
+                                                    "NEWT_PID_REMAP"))
         return (tuple(sorted((k, repr(v)) for k, v in constexprs.items())),
                 tuple((n, t.name, s) for n, (t, s) in types.items()),
                 num_warps, num_stages, env)

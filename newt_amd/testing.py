@@ -1,8 +1,15 @@
 """Benchmark helpers: event timing with a cache flush between reps.
 
-Same API as the reference (newt/testing.py:6-34). The flush buffer is 512 MiB:
-MI355X's 256 MiB Infinity Cache would hold the reference's 256 MiB flush
-entirely, so rep after rep would run from cache.
+Same API as the reference (newt/testing.py:6-34), two MI355X differences:
+  * the flush buffer is 512 MiB: MI355X's 256 MiB Infinity Cache (MALL) would
+    hold the reference's 256 MiB flush entirely, so rep after rep would run
+    from cache;
+  * the flush READS the buffer instead of zeroing it. L2 and MALL are
+    write-back: a 512 MiB zero fill leaves them full of dirty lines, and
+    writing those back to HBM competes with the kernel being timed (a plain
+    256 MiB device copy measured 25 % slower after a zero fill than after a
+    read). A read evicts the kernel's inputs just as well and leaves clean
+    lines, so the timed kernel sees cold, HBM-resident inputs only.
 """
 
 import torch
@@ -15,7 +22,7 @@ def _flush_buffer():
     dev = torch.cuda.current_device()
     buf = _flush.get(dev)
     if buf is None:
-        buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+        buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda")
         _flush[dev] = buf
     return buf
 
@@ -32,7 +39,7 @@ def do_bench(fn, warmup=10, rep=50, quantile=0.5, flush=True):
     end = [torch.cuda.Event(enable_timing=True) for _ in range(rep)]
     for i in range(rep):
         if cache is not None:
-            cache.zero_()
+            cache.sum()
         start[i].record()
         fn()
         end[i].record()
