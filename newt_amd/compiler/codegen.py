@@ -593,8 +593,10 @@ class Codegen(ast.NodeVisitor):
                     return L
         return self.default_layout(shape)
 
-    def elementwise(self, node, operands, rdtype, fn, meta=None):
-        """Apply fn (list of C exprs -> C expr) elementwise over broadcast operands."""
+    def elementwise(self, node, operands, rdtype, fn, meta=None, fast=None):
+        """Apply fn (list of C exprs -> C expr) elementwise over broadcast operands.
+        fast=(uniform C condition, fn2): when the result lands in registers,
+        fn2 replaces fn under the condition (a scalar branch per block)."""
         shape = ()
         for o in operands:
             if isinstance(o, Block):
@@ -617,9 +619,20 @@ class Codegen(ast.NodeVisitor):
             L = self.pick_layout(ops, shape)
         ops = [self.prepare(o, L) if isinstance(o, Block) else o for o in ops]
         out = self.new_reg(rdtype, shape, L)
+        if fast is not None:
+            self.emit(f"if ({fast[0]}) {{")
+            self.indent += 1
+            for s in range(L.nslots):
+                self.emit(f"{out.at(s)} = {fast[1]([self.ev(o, L, s) for o in ops])};")
+            self.indent -= 1
+            self.emit("} else {")
+            self.indent += 1
         for s in range(L.nslots):
             exprs = [self.ev(o, L, s) for o in ops]
             self.emit(f"{out.at(s)} = {fn(exprs)};")
+        if fast is not None:
+            self.indent -= 1
+            self.emit("}")
         return out
 
     def cast_block(self, v, dt):
@@ -1701,8 +1714,16 @@ class Codegen(ast.NodeVisitor):
         if isinstance(cond, Const):
             return a if cond.pyval else b
         rd = tp.promote(self.cdtype(a), self.cdtype(b))
+        fast = None
+        if isinstance(cond, Block):
+            # a mask that one uniform test proves all-true (interior tiles of a
+            # bounds or causal mask) selects `a` without per-element compares
+            full = self.mask_all_true(cond, cond.shape)
+            if full not in (None, "true", "false"):
+                fast = (full, lambda es: self.to_compute(es[1], a, rd))
         return self.elementwise(node, [cond, a, b], rd, lambda es: (
-            f"(({es[0]}) ? ({self.to_compute(es[1], a, rd)}) : ({self.to_compute(es[2], b, rd)}))"))
+            f"(({es[0]}) ? ({self.to_compute(es[1], a, rd)}) : ({self.to_compute(es[2], b, rd)}))"),
+            fast=fast)
 
     def op_cdiv(self, node, a, b):
         if isinstance(a, Const) and isinstance(b, Const):

@@ -11,7 +11,10 @@ reference's examples/01-05), extended to the BASELINE configurations:
   attention_kernel  examples/05_fused_attention.py:14-48 generalised to
                     [batch, heads, seq, head_dim] with a batch*head grid axis,
                     strides, an optional causal mask with the loop bound trimmed
-                    to the diagonal, and p cast to V's dtype before P @ V
+                    to the diagonal, p cast to V's dtype before P @ V, and the
+                    softmax written on exp2 with log2(e) folded into the scale
+                    (exp(x) = exp2(x*log2 e): the same softmax, fewer
+                    instructions per element)
 Everything is compiled by newt_amd's compiler to HIP for gfx950.
 """
 
@@ -191,6 +194,7 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
     qmask = offs_m[:, None] < S
     q = nl.load(q_base + offs_m[:, None] * sqm + offs_d[None, :], mask=qmask, other=0.0)
 
+    qk_scale = scale * 1.4426950408889634  # log2(e): the softmax runs on exp2
     m_i = nl.full((BLOCK_M,), float("-inf"), dtype=nl.float32)
     l_i = nl.zeros((BLOCK_M,), dtype=nl.float32)
     acc = nl.zeros((BLOCK_M, D), dtype=nl.float32)
@@ -202,15 +206,15 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
         offs_n = start_n + nl.arange(0, BLOCK_N)
         nmask = offs_n[:, None] < S
         k = nl.load(k_base + offs_n[:, None] * skn + offs_d[None, :], mask=nmask, other=0.0)
-        qk = nl.dot(q, nl.trans(k)) * scale
+        qk = nl.dot(q, nl.trans(k)) * qk_scale
         if CAUSAL:
             qk = nl.where((offs_m[:, None] >= offs_n[None, :]) & (offs_n[None, :] < S),
                           qk, float("-inf"))
         else:
             qk = nl.where(offs_n[None, :] < S, qk, float("-inf"))
         m_new = nl.maximum(m_i, nl.max(qk, axis=1))
-        alpha = nl.exp(m_i - m_new)
-        p = nl.exp(qk - m_new[:, None])
+        alpha = nl.exp2(m_i - m_new)
+        p = nl.exp2(qk - m_new[:, None])
         l_i = l_i * alpha + nl.sum(p, axis=1)
         acc = acc * alpha[:, None]
         v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :], mask=nmask, other=0.0)
