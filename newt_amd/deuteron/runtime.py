@@ -1,0 +1,285 @@
+"""deuteron runtime: trace -> newt source -> correctness-gated autotune -> launch.
+
+Protocol of the reference (deuteron/runtime.py:1-311):
+  1. the kernel function run eagerly (full-size tiles = plain PyTorch) on
+     clones of the arguments is the correctness oracle;
+  2. the newt source is generated once per argument signature (ranks, dtypes);
+     tile sizes are constexprs, so every configuration reuses it;
+  3. candidate configurations are launched, wrong results rejected
+     (tolerance 2e-2 for half precision or dot kernels, else 1e-3), the rest
+     timed with do_bench: a seeded random sample, then up to three rounds of
+     neighbour search around the best;
+  4. the winner is cached in memory and in ~/.deuteron/configs.json
+     (DEUTERON_CACHE_DIR) under name:source-hash:pow2-shapes:dtypes.
+
+The search space is this backend's: tile sizes that map onto 32x32 MFMA tiles
+for dot kernels, num_warps counted in 64-wide waves, and num_stages for the
+software-pipelined k-loop.
+"""
+
+import ast
+import hashlib
+import inspect
+import itertools
+import json
+import linecache
+import os
+import random
+import textwrap
+
+import torch
+
+from . import tracer
+from .language import EagerTensor
+
+_DOT_BLOCKS = [32, 64, 128, 256]
+_ELT_BLOCKS = [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096]
+
+
+def _cache_file():
+    d = os.environ.get("DEUTERON_CACHE_DIR") or os.path.join(os.path.expanduser("~"), ".deuteron")
+    os.makedirs(d, exist_ok=True)
+    return os.path.join(d, "configs.json")
+
+
+def _pow2(n):
+    n = int(n)
+    return 1 if n <= 1 else 1 << (n - 1).bit_length()
+
+
+class Config(dict):
+    """A configuration: BLOCK_<TILE> sizes plus num_warps / num_stages."""
+
+    @property
+    def num_warps(self):
+        return self.get("num_warps", 4)
+
+
+class Kernel:
+    def __init__(self, fn, config=None, autotune=True, samples=12, verbose=False):
+        self.fn = fn
+        self.__name__ = fn.__name__
+        self.fndef = ast.parse(textwrap.dedent(inspect.getsource(fn))).body[0]
+        self.fixed_config = Config(config) if config else None
+        self.autotune_enabled = autotune and config is None
+        self.samples = samples
+        self.verbose = verbose or bool(os.environ.get("DEUTERON_VERBOSE"))
+        self._ks = None
+        self._ks_sig = None
+        self._jit = None
+        self._configs = {}
+
+    # ------------------------------------------------------------ public API
+    def __call__(self, *args):
+        if os.environ.get("DEUTERON_INTERPRET"):
+            return self._eager(args)
+        ks = self._source_for(args)
+        cfg = self.fixed_config or self._get_config(ks, args)
+        self._launch(ks, args, cfg)
+
+    def ref(self, *args):
+        """Run the eager PyTorch reference (the oracle)."""
+        return self._eager(args)
+
+    def to_newt_source(self, *args):
+        """The generated newt kernel source for these example arguments."""
+        return self._source_for(args).source
+
+    @property
+    def best_config(self):
+        vals = list(self._configs.values())
+        return vals[-1] if vals else self.fixed_config
+
+    # ------------------------------------------------------------- internals
+    def _eager(self, args):
+        return self.fn(*[EagerTensor(a) if torch.is_tensor(a) else a for a in args])
+
+    @staticmethod
+    def _signature(args):
+        return tuple((a.dim(), str(a.dtype)) if torch.is_tensor(a) else type(a).__name__
+                     for a in args)
+
+    def _source_for(self, args):
+        sig = self._signature(args)
+        if self._ks is None or self._ks_sig != sig:
+            ks = tracer.generate(self.fn, self.fndef, args)
+            fname = f"<deuteron:{self.__name__}:{hashlib.sha256(ks.source.encode()).hexdigest()[:8]}>"
+            # newt reads kernel source with inspect.getsource: register it
+            linecache.cache[fname] = (len(ks.source), None, ks.source.splitlines(True), fname)
+            ns = {}
+            exec(compile(ks.source, fname, "exec"), ns)
+            self._ks, self._ks_sig, self._jit = ks, sig, ns[ks.name]
+            if self.verbose:
+                print(f"=== deuteron: generated newt source for {self.__name__} ===")
+                print(ks.source)
+        return self._ks
+
+    def _sizes(self, ks, args):
+        by = dict(zip([a.arg for a in self.fndef.args.args], args))
+        sizes = {}
+        for kind, nm in ks.params:
+            if kind == "tensor":
+                for d, s in enumerate(by[nm].shape):
+                    sizes[f"{nm}_d{d}"] = int(s)
+            else:
+                sizes[nm] = by[nm]
+        return sizes
+
+    def _args(self, ks, args):
+        by = dict(zip([a.arg for a in self.fndef.args.args], args))
+        out = []
+        for kind, nm in ks.params:
+            v = by[nm]
+            out.append(v)
+            if kind == "tensor":
+                out += [int(s) for s in v.shape] + [int(s) for s in v.stride()]
+        return out
+
+    @staticmethod
+    def _size(sizes, sym):
+        return int(sizes[sym]) if sym in sizes else int(sym)
+
+    def _constexprs(self, ks, sizes, cfg):
+        return {td.block: (_pow2(self._size(sizes, td.size)) if td.kind == "full" else cfg[td.block])
+                for td in ks.tile_vars}
+
+    def _launch(self, ks, args, cfg):
+        sizes = self._sizes(ks, args)
+        kw = self._constexprs(ks, sizes, cfg)
+        grid = tuple(-(-self._size(sizes, td.size) // kw[td.block]) for td in ks.grid_tiles)
+        self._jit[grid](*self._args(ks, args), **kw, num_warps=cfg.num_warps,
+                        num_stages=cfg.get("num_stages", 3))
+
+    # ------------------------------------------------------------ autotuning
+    def _key(self, ks, args):
+        h = hashlib.sha256(ks.source.encode()).hexdigest()[:12]
+        shapes = tuple(tuple(_pow2(s) for s in a.shape) if torch.is_tensor(a) else None
+                       for a in args)
+        dts = tuple(str(a.dtype) if torch.is_tensor(a) else "" for a in args)
+        return f"{self.__name__}:{h}:{shapes}:{dts}"
+
+    def _get_config(self, ks, args):
+        key = self._key(ks, args)
+        cfg = self._configs.get(key)
+        if cfg is not None:
+            return cfg
+        try:
+            with open(_cache_file()) as f:
+                disk = json.load(f)
+        except (OSError, ValueError):
+            disk = {}
+        if key in disk:
+            cfg = Config(disk[key])
+        else:
+            cfg = self._autotune(ks, args)
+            disk[key] = dict(cfg)
+            try:
+                with open(_cache_file(), "w") as f:
+                    json.dump(disk, f, indent=1)
+            except OSError:
+                pass
+        self._configs[key] = cfg
+        return cfg
+
+    @staticmethod
+    def _has_dot(ks):
+        return "nl.dot(" in ks.source
+
+    def _space(self, ks):
+        dot = self._has_dot(ks)
+        space = {nm: (_DOT_BLOCKS if dot else _ELT_BLOCKS) for nm in ks.tunable}
+        space["num_warps"] = [2, 4, 8] if dot else [1, 2, 4, 8]
+        if dot:
+            space["num_stages"] = [2, 3, 4]
+        return space
+
+    @staticmethod
+    def _neighbours(cfg, space):
+        out = []
+        for k, opts in space.items():
+            i = opts.index(cfg[k]) if cfg[k] in opts else 0
+            for j in (i - 1, i + 1):
+                if 0 <= j < len(opts):
+                    n = Config(cfg)
+                    n[k] = opts[j]
+                    out.append(n)
+        return out
+
+    def _autotune(self, ks, args):
+        from newt_amd.testing import do_bench
+
+        space = self._space(ks)
+        names = [a.arg for a in self.fndef.args.args]
+        # the oracle: the function run eagerly on clones
+        oracle = [a.clone() if torch.is_tensor(a) else a for a in args]
+        self._eager(oracle)
+        expected = {p: dict(zip(names, oracle))[p].clone() for p in ks.store_params}
+        work = [a.clone() if torch.is_tensor(a) else a for a in args]
+        outs = {p: dict(zip(names, work))[p] for p in ks.store_params}
+        initial = {p: dict(zip(names, args))[p] for p in ks.store_params}
+        dot = self._has_dot(ks)
+
+        def tol(t):
+            return 2e-2 if (t.dtype in (torch.float16, torch.bfloat16) or dot) else 1e-3
+
+        def attempt(cfg):
+            for p, o in outs.items():
+                o.copy_(initial[p])
+            try:
+                self._launch(ks, work, cfg)
+                torch.cuda.synchronize()
+            except Exception as e:  # invalid configuration (too much LDS, ...)
+                if self.verbose:
+                    print(f"  {dict(cfg)}: invalid ({str(e).splitlines()[0][:100]})")
+                return None
+            for p, want in expected.items():
+                t = tol(want)
+                if not torch.allclose(outs[p].float(), want.float(), rtol=t, atol=t):
+                    if self.verbose:
+                        print(f"  {dict(cfg)}: WRONG RESULT (skipped)")
+                    return None
+            ms = do_bench(lambda: self._launch(ks, work, cfg), warmup=3, rep=10)
+            if self.verbose:
+                print(f"  {dict(cfg)}: {ms:.4f} ms")
+            return ms
+
+        keys = list(space)
+        every = [Config(zip(keys, vals)) for vals in itertools.product(*[space[k] for k in keys])]
+        rng = random.Random(0)
+        cands = every if len(every) <= self.samples else rng.sample(every, self.samples)
+        seen, results = set(), []
+        for cfg in cands:
+            sig = frozenset(cfg.items())
+            if sig in seen:
+                continue
+            seen.add(sig)
+            ms = attempt(cfg)
+            if ms is not None:
+                results.append((ms, cfg))
+        if not results:
+            raise RuntimeError(f"deuteron: no valid config found for {self.__name__} "
+                               f"(try DEUTERON_VERBOSE=1)")
+        best_ms, best = min(results, key=lambda r: r[0])
+        for _ in range(3):
+            improved = False
+            for n in self._neighbours(best, space):
+                sig = frozenset(n.items())
+                if sig in seen:
+                    continue
+                seen.add(sig)
+                ms = attempt(n)
+                if ms is not None and ms < best_ms:
+                    best_ms, best, improved = ms, n, True
+            if not improved:
+                break
+        if self.verbose:
+            print(f"deuteron: {self.__name__} best {dict(best)} = {best_ms:.4f} ms")
+        return best
+
+
+def kernel(fn=None, *, config=None, autotune=True, samples=12, verbose=False):
+    """@deuteron.kernel: compile a tile-DSL function to autotuned newt kernels."""
+    if fn is None:
+        return lambda f: Kernel(f, config=config, autotune=autotune, samples=samples,
+                                verbose=verbose)
+    return Kernel(fn)
