@@ -641,8 +641,7 @@ class Codegen(ast.NodeVisitor):
 
     # ----------------------------------------------------------------- compile
     def compile(self):
-        for stmt in self.fndef.body:
-            self.visit(stmt)
+        self.visit_body(self.fndef.body)
         self.flush_loads()
         return self.assemble()
 

@@ -1,0 +1,539 @@
+"""Every nl.* operation on the GPU against torch, at the reference's tolerances.
+
+Semantics pinned here follow the reference's op suite (tests/test_ops.py):
+  elementwise binary ops in fp32 (rtol 1e-5) and fp16 (2e-3)       :21-68
+  int32 bit ops, shifts, C-truncating % and // (exact)             :71-117
+  unary math (rtol/atol 1e-5)                                      :120-178
+  casts (float within 1e-3, int exact)                             :181-210
+  axis and full reductions, fp16 sums accumulating in fp32         :213-289
+  broadcast / broadcast_to / reshape / trans (exact)               :292-337
+  strided, gathered and scalar loads (exact)                       :340-391
+  atomics: histogram == bincount, int atomic_max                   :394-426
+  nl.dot shapes / dtypes / waves, dot epilogue                     :429-481
+The kernels are launched through the HIP backend (hipRTC code objects,
+libnewt_hip.so); torch on the same device is the oracle.
+"""
+
+import pytest
+import torch
+
+import newt
+import newt.language as nl
+
+pytestmark = pytest.mark.gpu
+
+
+def rnd(shape, dtype=torch.float32, seed=0, positive=False):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(shape, device="cuda", generator=g)
+    if positive:
+        x = x.abs() + 0.5
+    return x.to(dtype)
+
+
+# --------------------------------------------------------------- elementwise
+
+@newt.jit
+def binary_k(x_ptr, y_ptr, o_ptr, n, OP: nl.constexpr, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    live = offs < n
+    a = nl.load(x_ptr + offs, mask=live)
+    b = nl.load(y_ptr + offs, mask=live, other=1.0)
+    if OP == "add":
+        r = a + b
+    elif OP == "sub":
+        r = a - b
+    elif OP == "mul":
+        r = a * b
+    elif OP == "div":
+        r = a / b
+    elif OP == "pow2":
+        r = a ** 2
+    elif OP == "maximum":
+        r = nl.maximum(a, b)
+    elif OP == "minimum":
+        r = nl.minimum(a, b)
+    elif OP == "fma":
+        r = nl.fma(a, b, a)
+    else:
+        r = nl.where(a > 0, a, b)
+    nl.store(o_ptr + offs, r, mask=live)
+
+
+TORCH_BINARY = {
+    "add": torch.add,
+    "sub": torch.sub,
+    "mul": torch.mul,
+    "div": torch.div,
+    "pow2": lambda a, b: a * a,
+    "maximum": torch.maximum,
+    "minimum": torch.minimum,
+    "fma": lambda a, b: a * b + a,
+    "where": lambda a, b: torch.where(a > 0, a, b),
+}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("op", sorted(TORCH_BINARY))
+def test_binary(op, dtype):
+    n = 4321
+    a, b = rnd(n, dtype, 0), rnd(n, dtype, 1, positive=True)
+    o = torch.empty_like(a)
+    binary_k[(newt.cdiv(n, 1024),)](a, b, o, n, OP=op, BLOCK=1024)
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    torch.testing.assert_close(o.float(), TORCH_BINARY[op](a, b).float(), rtol=tol, atol=tol)
+
+
+@newt.jit
+def int_k(x_ptr, y_ptr, o_ptr, n, OP: nl.constexpr, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    live = offs < n
+    a = nl.load(x_ptr + offs, mask=live)
+    b = nl.load(y_ptr + offs, mask=live, other=1)
+    if OP == "and":
+        r = a & b
+    elif OP == "or":
+        r = a | b
+    elif OP == "xor":
+        r = a ^ b
+    elif OP == "shl":
+        r = a << 1
+    elif OP == "shr":
+        r = a >> 2
+    elif OP == "mod":
+        r = a % b
+    else:
+        r = a // b
+    nl.store(o_ptr + offs, r, mask=live)
+
+
+def _c_div(a, b):
+    return torch.div(a, b, rounding_mode="trunc")
+
+
+TORCH_INT = {
+    "and": torch.bitwise_and,
+    "or": torch.bitwise_or,
+    "xor": torch.bitwise_xor,
+    "shl": lambda a, b: a << 1,
+    "shr": lambda a, b: a >> 2,
+    "mod": lambda a, b: a - _c_div(a, b) * b,   # C remainder (sign of the dividend)
+    "floordiv": _c_div,                         # C truncation
+}
+
+
+@pytest.mark.parametrize("signed", [False, True])
+@pytest.mark.parametrize("op", sorted(TORCH_INT))
+def test_int32(op, signed):
+    n = 2048
+    g = torch.Generator(device="cuda").manual_seed(3)
+    a = torch.randint(-1000 if signed else 0, 1000, (n,), device="cuda", generator=g,
+                      dtype=torch.int32)
+    b = torch.randint(1, 50, (n,), device="cuda", generator=g, dtype=torch.int32)
+    if signed:
+        b = torch.where(torch.arange(n, device="cuda") % 3 == 0, -b, b)
+    o = torch.empty_like(a)
+    int_k[(newt.cdiv(n, 1024),)](a, b, o, n, OP=op, BLOCK=1024)
+    assert torch.equal(o, TORCH_INT[op](a, b))
+
+
+@newt.jit
+def unary_k(x_ptr, o_ptr, n, OP: nl.constexpr, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    live = offs < n
+    v = nl.load(x_ptr + offs, mask=live, other=1.0)
+    if OP == "exp":
+        r = nl.exp(v)
+    elif OP == "exp2":
+        r = nl.exp2(v)
+    elif OP == "log":
+        r = nl.log(v)
+    elif OP == "log2":
+        r = nl.log2(v)
+    elif OP == "sqrt":
+        r = nl.sqrt(v)
+    elif OP == "rsqrt":
+        r = nl.rsqrt(v)
+    elif OP == "sin":
+        r = nl.sin(v)
+    elif OP == "cos":
+        r = nl.cos(v)
+    elif OP == "tanh":
+        r = nl.tanh(v)
+    elif OP == "erf":
+        r = nl.erf(v)
+    elif OP == "sigmoid":
+        r = nl.sigmoid(v)
+    elif OP == "abs":
+        r = nl.abs(v)
+    elif OP == "floor":
+        r = nl.floor(v)
+    elif OP == "ceil":
+        r = nl.ceil(v)
+    else:
+        r = -v
+    nl.store(o_ptr + offs, r, mask=live)
+
+
+TORCH_UNARY = {
+    "exp": torch.exp, "exp2": torch.exp2, "log": torch.log, "log2": torch.log2,
+    "sqrt": torch.sqrt, "rsqrt": torch.rsqrt, "sin": torch.sin, "cos": torch.cos,
+    "tanh": torch.tanh, "erf": torch.erf, "sigmoid": torch.sigmoid, "abs": torch.abs,
+    "floor": torch.floor, "ceil": torch.ceil, "neg": torch.neg,
+}
+
+
+@pytest.mark.parametrize("op", sorted(TORCH_UNARY))
+def test_unary(op):
+    n = 3000
+    x = rnd(n, positive=op in ("log", "log2", "sqrt", "rsqrt"))
+    o = torch.empty_like(x)
+    unary_k[(newt.cdiv(n, 1024),)](x, o, n, OP=op, BLOCK=1024)
+    torch.testing.assert_close(o, TORCH_UNARY[op](x), rtol=1e-5, atol=1e-5)
+
+
+@newt.jit
+def cast_k(x_ptr, o_ptr, n, DT: nl.constexpr, BLOCK: nl.constexpr):
+    offs = nl.arange(0, BLOCK)
+    live = offs < n
+    nl.store(o_ptr + offs, nl.load(x_ptr + offs, mask=live).to(DT), mask=live)
+
+
+@pytest.mark.parametrize("src,dst,ndt", [
+    (torch.float32, torch.float16, nl.float16),
+    (torch.float16, torch.float32, nl.float32),
+    (torch.float32, torch.bfloat16, nl.bfloat16),
+    (torch.bfloat16, torch.float32, nl.float32),
+    (torch.float32, torch.int32, nl.int32),
+    (torch.int32, torch.float32, nl.float32),
+    (torch.int64, torch.int32, nl.int32),
+    (torch.int32, torch.int64, nl.int64),
+])
+def test_cast(src, dst, ndt):
+    n = 1000
+    x = (rnd(n, seed=4) * 10).to(src)
+    o = torch.empty(n, device="cuda", dtype=dst)
+    cast_k[(1,)](x, o, n, DT=ndt, BLOCK=1024)
+    want = x.to(dst)
+    if dst.is_floating_point:
+        torch.testing.assert_close(o.float(), want.float(), rtol=1e-3, atol=1e-3)
+    else:
+        assert torch.equal(o, want)
+
+
+def test_cast_rounds_to_nearest_even():
+    """fp32 -> fp16/bf16 conversions round to nearest even, as torch does."""
+    x = torch.randn(1 << 14, device="cuda") * 3
+    for dt, ndt in ((torch.float16, nl.float16), (torch.bfloat16, nl.bfloat16)):
+        o = torch.empty(x.numel(), device="cuda", dtype=dt)
+        for i in range(0, x.numel(), 1024):
+            cast_k[(1,)](x[i:], o[i:], 1024, DT=ndt, BLOCK=1024)
+        assert torch.equal(o, x.to(dt))
+
+
+# ---------------------------------------------------------------- reductions
+
+@newt.jit
+def reduce2d_k(x_ptr, o_ptr, M, N, sx, OP: nl.constexpr, AXIS: nl.constexpr,
+               BM: nl.constexpr, BN: nl.constexpr):
+    rm = nl.arange(0, BM)
+    rn = nl.arange(0, BN)
+    inb = (rm[:, None] < M) & (rn[None, :] < N)
+    ptrs = x_ptr + rm[:, None] * sx + rn[None, :]
+    if OP == "sum":
+        r = nl.sum(nl.load(ptrs, mask=inb, other=0.0), axis=AXIS)
+    elif OP == "max":
+        r = nl.max(nl.load(ptrs, mask=inb, other=float("-inf")), axis=AXIS)
+    else:
+        r = nl.min(nl.load(ptrs, mask=inb, other=float("inf")), axis=AXIS)
+    if AXIS == 0:
+        nl.store(o_ptr + rn, r, mask=rn < N)
+    else:
+        nl.store(o_ptr + rm, r, mask=rm < M)
+
+
+@pytest.mark.parametrize("mn", [(32, 64), (17, 100), (128, 128), (3, 1000), (300, 5)])
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("op", ["sum", "max", "min"])
+def test_reduce_axis(op, axis, mn):
+    M, N = mn
+    x = rnd((M, N), seed=5)
+    o = torch.empty(N if axis == 0 else M, device="cuda")
+    reduce2d_k[(1,)](x, o, M, N, x.stride(0), OP=op, AXIS=axis,
+                     BM=newt.next_power_of_2(M), BN=newt.next_power_of_2(N))
+    want = {"sum": x.sum(axis), "max": x.amax(axis), "min": x.amin(axis)}[op]
+    torch.testing.assert_close(o, want, rtol=1e-4, atol=1e-4)
+
+
+@newt.jit
+def reduce_full_k(x_ptr, o_ptr, n, OP: nl.constexpr, BLOCK: nl.constexpr):
+    offs = nl.arange(0, BLOCK)
+    live = offs < n
+    if OP == "sum":
+        r = nl.sum(nl.load(x_ptr + offs, mask=live, other=0.0))
+    elif OP == "max":
+        r = nl.max(nl.load(x_ptr + offs, mask=live, other=float("-inf")))
+    else:
+        r = nl.min(nl.load(x_ptr + offs, mask=live, other=float("inf")))
+    nl.store(o_ptr, r)
+
+
+@pytest.mark.parametrize("waves", [1, 4, 8, 16])
+@pytest.mark.parametrize("n", [32, 100, 1024, 5000])
+@pytest.mark.parametrize("op", ["sum", "max", "min"])
+def test_reduce_full(op, n, waves):
+    x = rnd(n, seed=6)
+    o = torch.empty(1, device="cuda")
+    reduce_full_k[(1,)](x, o, n, OP=op, BLOCK=newt.next_power_of_2(n), num_warps=waves)
+    want = {"sum": x.sum(), "max": x.max(), "min": x.min()}[op]
+    torch.testing.assert_close(o[0], want, rtol=1e-4, atol=1e-4)
+
+
+@newt.jit
+def sum_all_k(x_ptr, o_ptr, BLOCK: nl.constexpr):
+    nl.store(o_ptr, nl.sum(nl.load(x_ptr + nl.arange(0, BLOCK))))
+
+
+def test_fp16_sum_accumulates_in_fp32():
+    # 4096 fp16 ones: an fp16 accumulator would stall at 2048
+    x = torch.ones(4096, device="cuda", dtype=torch.float16)
+    o = torch.empty(1, device="cuda")
+    sum_all_k[(1,)](x, o, BLOCK=4096)
+    assert o.item() == 4096.0
+
+
+@newt.jit
+def int_reduce_k(x_ptr, o_ptr, BLOCK: nl.constexpr):
+    v = nl.load(x_ptr + nl.arange(0, BLOCK))
+    nl.store(o_ptr, nl.sum(v))
+    nl.store(o_ptr + 1, nl.max(v))
+    nl.store(o_ptr + 2, nl.min(v))
+
+
+def test_int_reductions_exact():
+    x = torch.randint(-10**6, 10**6, (2048,), device="cuda", dtype=torch.int32)
+    o = torch.empty(3, device="cuda", dtype=torch.int32)
+    int_reduce_k[(1,)](x, o, BLOCK=2048)
+    assert o.tolist() == [int(x.sum()), int(x.max()), int(x.min())]
+
+
+# ------------------------------------------------------------- shape ops
+
+@newt.jit
+def outer_k(a_ptr, b_ptr, o_ptr, BM: nl.constexpr, BN: nl.constexpr):
+    a = nl.load(a_ptr + nl.arange(0, BM))
+    b = nl.load(b_ptr + nl.arange(0, BN))
+    grid = nl.arange(0, BM)[:, None] * BN + nl.arange(0, BN)[None, :]
+    nl.store(o_ptr + grid, a[:, None] * 100 + b[None, :])
+
+
+def test_broadcast_outer():
+    a, b = rnd(32), rnd(64, seed=1)
+    o = torch.empty(32, 64, device="cuda")
+    outer_k[(1,)](a, b, o, BM=32, BN=64)
+    torch.testing.assert_close(o, a[:, None] * 100 + b[None, :], rtol=1e-5, atol=1e-5)
+
+
+@newt.jit
+def bcast_reshape_k(a_ptr, o_ptr, BM: nl.constexpr, BN: nl.constexpr):
+    a = nl.load(a_ptr + nl.arange(0, BM))
+    full = nl.broadcast_to(a[:, None], (BM, BN))
+    nl.store(o_ptr + nl.arange(0, BM * BN), nl.reshape(full, (BM * BN,)))
+
+
+def test_broadcast_to_then_reshape():
+    a = rnd(16)
+    o = torch.empty(16 * 32, device="cuda")
+    bcast_reshape_k[(1,)](a, o, BM=16, BN=32)
+    assert torch.equal(o.view(16, 32), a[:, None].expand(16, 32))
+
+
+@newt.jit
+def trans_k(x_ptr, o_ptr, BM: nl.constexpr, BN: nl.constexpr):
+    x = nl.load(x_ptr + nl.arange(0, BM)[:, None] * BN + nl.arange(0, BN)[None, :])
+    nl.store(o_ptr + nl.arange(0, BN)[:, None] * BM + nl.arange(0, BM)[None, :], nl.trans(x))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("mn", [(32, 64), (64, 32), (128, 8), (16, 16)])
+def test_trans(mn, dtype):
+    M, N = mn
+    x = rnd((M, N), dtype)
+    o = torch.empty(N, M, device="cuda", dtype=dtype)
+    trans_k[(1,)](x, o, BM=M, BN=N)
+    assert torch.equal(o, x.t().contiguous())
+
+
+# ---------------------------------------------------------- loads and stores
+
+@newt.jit
+def strided_k(x_ptr, o_ptr, n, sx, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    live = offs < n
+    nl.store(o_ptr + offs, nl.load(x_ptr + offs * sx, mask=live) * 2, mask=live)
+
+
+def test_strided_load():
+    base = rnd(2000)
+    view = base[::2]
+    o = torch.empty(view.numel(), device="cuda")
+    strided_k[(newt.cdiv(view.numel(), 256),)](base, o, view.numel(), 2, BLOCK=256)
+    assert torch.equal(o, view * 2)
+
+
+@newt.jit
+def gather_k(x_ptr, idx_ptr, o_ptr, n, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    live = offs < n
+    i = nl.load(idx_ptr + offs, mask=live)
+    nl.store(o_ptr + offs, nl.load(x_ptr + i, mask=live), mask=live)
+
+
+def test_gather():
+    n = 4096
+    x = rnd(n)
+    idx = torch.randperm(n, device="cuda").to(torch.int32)
+    o = torch.empty(n, device="cuda")
+    gather_k[(newt.cdiv(n, 1024),)](x, idx, o, n, BLOCK=1024)
+    assert torch.equal(o, x[idx.long()])
+
+
+@newt.jit
+def scatter_k(x_ptr, idx_ptr, o_ptr, n, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    live = offs < n
+    i = nl.load(idx_ptr + offs, mask=live)
+    nl.store(o_ptr + i, nl.load(x_ptr + offs, mask=live), mask=live)
+
+
+def test_scatter():
+    n = 3000
+    x = rnd(n)
+    idx = torch.randperm(n, device="cuda").to(torch.int32)
+    o = torch.zeros(n, device="cuda")
+    scatter_k[(newt.cdiv(n, 512),)](x, idx, o, n, BLOCK=512)
+    want = torch.zeros_like(o)
+    want[idx.long()] = x
+    assert torch.equal(o, want)
+
+
+@newt.jit
+def scalar_load_k(x_ptr, o_ptr, BLOCK: nl.constexpr):
+    s = nl.load(x_ptr)
+    nl.store(o_ptr + nl.arange(0, BLOCK), nl.zeros((BLOCK,), dtype=nl.float32) + s)
+
+
+def test_scalar_load():
+    x = torch.tensor([42.0], device="cuda")
+    o = torch.empty(128, device="cuda")
+    scalar_load_k[(1,)](x, o, BLOCK=128)
+    assert bool((o == 42.0).all())
+
+
+@newt.jit
+def misaligned_k(x_ptr, o_ptr, n, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    live = offs < n
+    nl.store(o_ptr + offs, nl.load(x_ptr + offs, mask=live) + 1.0, mask=live)
+
+
+@pytest.mark.parametrize("shift", [1, 2, 3])
+def test_unaligned_pointers_take_the_scalar_path(shift):
+    # views starting 4/8/12 bytes into an allocation defeat 16-byte vector access
+    base = rnd(5000)
+    x = base[shift:]
+    o = torch.zeros(5000, device="cuda")[shift:]
+    misaligned_k[(newt.cdiv(x.numel(), 1024),)](x, o, x.numel(), BLOCK=1024)
+    assert torch.equal(o, x + 1.0)
+
+
+# ------------------------------------------------------------------ atomics
+
+@newt.jit
+def histogram_k(idx_ptr, hist_ptr, n, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    live = offs < n
+    nl.atomic_add(hist_ptr + nl.load(idx_ptr + offs, mask=live), 1.0, mask=live)
+
+
+def test_atomic_add_histogram():
+    n, bins = 100_000, 64
+    idx = torch.randint(0, bins, (n,), device="cuda", dtype=torch.int32)
+    hist = torch.zeros(bins, device="cuda")
+    histogram_k[(newt.cdiv(n, 1024),)](idx, hist, n, BLOCK=1024)
+    assert torch.equal(hist, torch.bincount(idx.long(), minlength=bins).float())
+
+
+@newt.jit
+def block_max_k(x_ptr, o_ptr, n, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    v = nl.load(x_ptr + offs, mask=offs < n, other=0)
+    nl.atomic_max(o_ptr, nl.max(v))
+
+
+def test_atomic_max_int():
+    n = 10_000
+    x = torch.randint(0, 1_000_000, (n,), device="cuda", dtype=torch.int32)
+    o = torch.zeros(1, device="cuda", dtype=torch.int32)
+    block_max_k[(newt.cdiv(n, 1024),)](x, o, n, BLOCK=1024)
+    assert o.item() == x.max().item()
+
+
+# ---------------------------------------------------------------------- dot
+
+@newt.jit
+def dot_k(a_ptr, b_ptr, c_ptr, BM: nl.constexpr, BN: nl.constexpr, BK: nl.constexpr):
+    rm, rk, rn = nl.arange(0, BM), nl.arange(0, BK), nl.arange(0, BN)
+    a = nl.load(a_ptr + rm[:, None] * BK + rk[None, :])
+    b = nl.load(b_ptr + rk[:, None] * BN + rn[None, :])
+    nl.store(c_ptr + rm[:, None] * BN + rn[None, :], nl.dot(a, b))
+
+
+@pytest.mark.parametrize("waves", [1, 2, 4])
+@pytest.mark.parametrize("shape", [(16, 16, 16), (32, 64, 128), (64, 32, 16), (128, 128, 64)])
+@pytest.mark.parametrize("dtype,tol", [(torch.float16, 2e-2), (torch.bfloat16, 3e-2),
+                                       (torch.float32, 2e-2)])
+def test_dot(dtype, tol, shape, waves):
+    BM, BN, BK = shape
+    a = rnd((BM, BK), dtype) * 0.3
+    b = rnd((BK, BN), dtype, seed=1) * 0.3
+    c = torch.empty(BM, BN, device="cuda")
+    dot_k[(1,)](a, b, c, BM=BM, BN=BN, BK=BK, num_warps=waves)
+    torch.testing.assert_close(c, a.float() @ b.float(), rtol=tol, atol=tol)
+
+
+@newt.jit
+def dot_epilogue_k(a_ptr, b_ptr, o_ptr, BM: nl.constexpr, BN: nl.constexpr, BK: nl.constexpr):
+    rm, rk, rn = nl.arange(0, BM), nl.arange(0, BK), nl.arange(0, BN)
+    a = nl.load(a_ptr + rm[:, None] * BK + rk[None, :])
+    b = nl.load(b_ptr + rk[:, None] * BN + rn[None, :])
+    c = nl.dot(a, b) * 2.0 + 1.0
+    nl.store(o_ptr + rm, nl.sum(c, axis=1))
+    nl.store(o_ptr + BM + rn, nl.max(c, axis=0))
+
+
+def test_dot_epilogue_reductions():
+    a = rnd((32, 32), torch.float16) * 0.3
+    b = rnd((32, 32), torch.float16, seed=1) * 0.3
+    o = torch.empty(64, device="cuda")
+    dot_epilogue_k[(1,)](a, b, o, BM=32, BN=32, BK=32)
+    c = a.float() @ b.float() * 2 + 1
+    torch.testing.assert_close(o[:32], c.sum(1), rtol=2e-2, atol=2e-1)
+    torch.testing.assert_close(o[32:], c.amax(0), rtol=2e-2, atol=2e-2)
+
+
+@newt.jit
+def dot_trans_k(a_ptr, b_ptr, c_ptr, BM: nl.constexpr, BN: nl.constexpr, BK: nl.constexpr):
+    rm, rk, rn = nl.arange(0, BM), nl.arange(0, BK), nl.arange(0, BN)
+    a = nl.load(a_ptr + rm[:, None] * BK + rk[None, :])
+    bt = nl.load(b_ptr + rn[:, None] * BK + rk[None, :])   # B stored [N, K]
+    nl.store(c_ptr + rm[:, None] * BN + rn[None, :], nl.dot(a, nl.trans(bt)))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_dot_with_transposed_operand(dtype):
+    a = rnd((64, 64), dtype) * 0.3
+    bt = rnd((128, 64), dtype, seed=1) * 0.3
+    c = torch.empty(64, 128, device="cuda")
+    dot_trans_k[(1,)](a, bt, c, BM=64, BN=128, BK=64)
+    torch.testing.assert_close(c, a.float() @ bt.float().t(), rtol=2e-2, atol=2e-2)
