@@ -84,6 +84,61 @@ def _operand_name(a):
     return (a.id, trans) if isinstance(a, ast.Name) else (None, trans)
 
 
+def _kform(e, kinds):
+    """How expression e depends on the loop variable: 'c' not at all, 'a' affinely
+    (sums, differences, products with an invariant factor), 'b' as a conjunction
+    of comparisons between such terms (a condition that holds on an interval of
+    iterations), None in any other way. kinds maps loop-defined names to their
+    form (None for names of unknown form)."""
+    if isinstance(e, ast.Name):
+        return kinds.get(e.id, "c")
+    if isinstance(e, ast.Constant):
+        return "c"
+    if isinstance(e, ast.Subscript):
+        f = _kform(e.value, kinds)
+        return f if _kform(e.slice, kinds) == "c" else None
+    if isinstance(e, (ast.Tuple, ast.Slice)):
+        parts = [p for p in ast.iter_child_nodes(e) if isinstance(p, ast.expr)]
+        return "c" if all(_kform(p, kinds) == "c" for p in parts) else None
+    if isinstance(e, ast.UnaryOp):
+        f = _kform(e.operand, kinds)
+        if isinstance(e.op, (ast.USub, ast.UAdd)) and f != "b":
+            return f
+        return "c" if f == "c" else None
+    if isinstance(e, ast.BinOp):
+        fl, fr = _kform(e.left, kinds), _kform(e.right, kinds)
+        if fl is None or fr is None:
+            return None
+        if fl == "c" and fr == "c":
+            return "c"
+        if isinstance(e.op, ast.BitAnd):
+            return "b" if {fl, fr} <= {"b", "c"} else None
+        if "b" in (fl, fr):
+            return None
+        if isinstance(e.op, (ast.Add, ast.Sub)):
+            return "a"
+        if isinstance(e.op, ast.Mult) and "c" in (fl, fr):
+            return "a"
+        return None
+    if isinstance(e, ast.Compare):
+        forms = [_kform(x, kinds) for x in [e.left] + list(e.comparators)]
+        if all(f == "c" for f in forms):
+            return "c"
+        if (len(e.ops) == 1 and isinstance(e.ops[0], (ast.Lt, ast.LtE, ast.Gt, ast.GtE))
+                and all(f in ("a", "c") for f in forms)):
+            return "b"
+        return None
+    if isinstance(e, ast.BoolOp) and isinstance(e.op, ast.And):
+        forms = [_kform(x, kinds) for x in e.values]
+        if all(f == "c" for f in forms):
+            return "c"
+        return "b" if all(f in ("b", "c") for f in forms) else None
+    if isinstance(e, (ast.Call, ast.Attribute)):
+        parts = [p for p in ast.walk(e) if isinstance(p, ast.Name)]
+        return "c" if all(kinds.get(p.id, "c") == "c" for p in parts) else None
+    return None
+
+
 class DotPipeline:
     # ------------------------------------------------------------ detection
     def _const_test(self, test):
@@ -223,9 +278,25 @@ class DotPipeline:
         # not be defined before it
         if any(t in self.locals or t in self.storages for t in konly):
             return None
+        # form of each staged mask in the loop variable: conjunctions of affine
+        # comparisons hold on an interval of iterations, which lets the loop be
+        # versioned on a test of its first and last iterations
+        kinds = {kname: "a"}
+        for nm in carried:
+            kinds[nm] = None
+        for s in flat:
+            nm = _target(s)
+            if nm in konly:
+                kinds[nm] = _kform(s.value, kinds)
+        fast_ok = True
+        for rec in staged.values():
+            call = flat[rec["index"]].value
+            masks = [k.value for k in call.keywords if k.arg == "mask"] + list(call.args[1:2])
+            if any(_kform(m, kinds) not in ("b", "c") for m in masks):
+                fast_ok = False
         return {"flat": flat, "staged": staged, "slice": sorted(slice_idx),
                 "advance": sorted(assigned[nm][0] for nm in carried), "konly": konly,
-                "kname": kname, "node": node}
+                "kname": kname, "node": node, "fast_ok": fast_ok}
 
     # ----------------------------------------------------------- emission
     def pipelined_for(self, node, plan, lo_, hi, st, idt):
@@ -241,6 +312,15 @@ class DotPipeline:
         n = self.new_scalar(idt, f"((({hi_e}) > ({lo_e})) ? ((({hi_e}) - ({lo_e}) + {stv - 1}) "
                                  f"/ {stv}) : 0)")
         state = {"node": node, "S": S, "recs": None, "plan": plan}
+        compute = [x for i, x in enumerate(flat) if i not in skip and i not in plan["slice"]]
+        ndots = sum(1 for x in compute for nd in ast.walk(x) if _callee(nd) == "dot")
+        # a k-loop that only accumulates one dot (matmul) reads the first k-step
+        # of the next stage's operands into registers before the barrier
+        simple = len(compute) == 1 and ndots == 1
+        plr_env = os.environ.get("NEWT_PLR", "auto")
+        state["plr"] = S >= 3 and (plr_env == "1" or (plr_env == "auto" and simple))
+        state["simple"] = simple
+        state["pf"] = {}
         self.pipe_records.append(state)
         for s in range(S - 1):
             self.locals[kname] = self.new_scalar(idt, f"({lo_e} + {s * stv})")
@@ -253,17 +333,146 @@ class DotPipeline:
         rec = self._enter_compound(node)
         self.drain_dots_for_loop(node)
         it0 = self.fresh("it")
-        self.emit(f"for ({idt.ctype} {it0} = 0; {it0} < {n.expr}; {it0} += {S}) {{")
+        self.emit(f"{idt.ctype} {it0} = 0;")
+        mark = len(self.lines)
+        ctx = (node, state, S, n, lo_e, stv, idt, slice_stmts, advance, skip, temps, kname, flat)
+        if plan["fast_ok"] and os.environ.get("NEWT_PIPE_VERSION", "1") != "0":
+            # leading iterations whose every tile is a whole in-bounds copy run
+            # in a copy of the loop with no per-iteration tests at all
+            nf = self._fast_count(ctx)
+            self.emit(f"for (; {it0} + {2 * S - 2} < {nf.expr}; {it0} += {S}) {{")
+            self._pipe_iterations(ctx, it0, fast=True)
+            self.emit("}")
+        self.emit(f"for (; {it0} < {n.expr}; {it0} += {S}) {{")
+        self._pipe_iterations(ctx, it0, fast=False)
+        self.emit("}")
+        if state["plr"]:
+            self._insert_lines(mark, self._plr_preamble(state, n))
+        self._exit_compound(rec)
+        self.after_loop(node)
+
+    def _insert_lines(self, index, lines):
+        ind = "  " * self.indent
+        self.lines[index:index] = [ind + ln for ln in lines]
+        for r in self.pending_hoist:
+            if r["index"] >= index:
+                r["index"] += len(lines)
+
+    def _plr_preamble(self, state, n):
+        """Declarations of the prefetched fragments and their first fill from
+        stage 0, once iterations 0 and 1 have landed."""
+        S, ops = state["S"], state["ops"]
+        out = []
+        for d, frags in sorted(state["pf"].items()):
+            for var, _ in frags:
+                out.append(f"i16x8 {var};")
+        deep = (S - 3) * ops
+        if deep:
+            out.append(f"if ({S - 2} < {n.expr}) newt::wait_vmcnt<{deep}>(); else newt::wait_vmcnt<0>();")
+        else:
+            out.append("newt::wait_vmcnt<0>();")
+        out.append("__syncthreads();")
+        for d, frags in sorted(state["pf"].items()):
+            for var, fn in frags:
+                out.append(f"{var} = {fn(0)};")
+        return out
+
+    def _plr_fill(self, state, slot):
+        for d, frags in sorted(state["pf"].items()):
+            for var, fn in frags:
+                self.emit(f"{var} = {fn(slot)};")
+
+    def _sched_hints(self, state):
+        """Interleave, in the straight-line fast loop, each k-step's MFMAs with
+        the LDS reads of the next k-step (the last k-step with the prefetch of
+        the next stage) and the first k-step's MFMAs with the stage copies."""
+        info = state.get("sched")
+        if not info:
+            return
+        reads, mfmas = info["reads"], info["mfmas"]
+        nks = len(reads)
+        fills = []
+        for t in range(nks):
+            f = [("0x100", 1)] * (reads[t + 1] if t + 1 < nks else reads[0])
+            if t == 0:
+                dma = [("0x020", 1)] * state["ops"]
+                # alternate copies and reads so neither queue starves
+                mixed = []
+                while f or dma:
+                    if dma:
+                        mixed.append(dma.pop(0))
+                    if f:
+                        mixed.append(f.pop(0))
+                f = mixed
+            fills.append(f)
+        for t in range(nks):
+            f = fills[t]
+            m = mfmas[t]
+            for i in range(m):
+                self.emit("__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
+                take = (len(f) + (m - i) - 1) // (m - i)
+                for mask, cnt in f[:take]:
+                    self.emit(f"__builtin_amdgcn_sched_group_barrier({mask}, {cnt}, 0);")
+                f = f[take:]
+
+    def _fast_count(self, ctx):
+        """Number of leading iterations j (from 0) whose DMA tiles are all
+        whole, in-bounds copies. Each such condition is a conjunction of
+        comparisons affine in j, so it holds on an interval: it holds for every
+        j < m+1 when it holds at j = 0 and at j = m. m = n-1 covers divisible
+        loops, m = n-2 a ragged last tile; otherwise no iteration is fast."""
+        node, state, S, n, lo_e, stv, idt, slice_stmts, advance, skip, temps, kname, flat = ctx
+        conds = []
+        for j in ("0", f"({n.expr} - 1)", f"({n.expr} - 2)"):
+            self.locals[kname] = self.new_scalar(idt, f"({lo_e} + {j} * {stv})")
+            self.visit_body(slice_stmts)
+            conds.append(self.pipe_dma_condition(state))
+            for t in temps:
+                self.locals.pop(t, None)
+        c0, c1, c2 = conds
+        return self.new_scalar(idt, f"(({c0}) ? (({c1}) ? {n.expr} : (({c2}) ? ({n.expr} - 1) : 0)) : 0)")
+
+    def pipe_dma_condition(self, state):
+        """Uniform condition under which every DMA tile of the slice just
+        visited is a whole in-bounds copy; consumes the slice's loads."""
+        if state["recs"] is None:
+            self._init_recs(state)
+        conds = []
+        for r in state["recs"].values():
+            X = self.locals.get(r["name"])
+            if not isinstance(X, LazyLoad) or X.result is not None or tuple(X.shape) != r["shape"]:
+                self._no_pipe(state)
+            if r["dma"]:
+                full = self.mask_all_true(X.mask, X.shape)
+                if full is not None and full != "true":
+                    conds.append(f"({full})")
+            X.consumed = True
+            if X in self.pending_loads:
+                self.pending_loads.remove(X)
+        return " && ".join(conds) if conds else "true"
+
+    def _pipe_iterations(self, ctx, it0, fast):
+        """One trip of the main loop: S sub-iterations, sub-iteration s computing
+        from stage s and issuing iteration it+S-1 into stage (s+S-1)%S. In the
+        fast copy every sub-iteration is known to run, to wait for exactly the
+        copies of S-2 later iterations, and to issue whole in-bounds tiles."""
+        node, state, S, n, lo_e, stv, idt, slice_stmts, advance, skip, temps, kname, flat = ctx
         self.indent += 1
         self.loop_depth += 1
         ops = state["ops"]
         self.pipe_active = state
+        plr = state["plr"]
+        state["fast"] = fast
         for s in range(S):
             it = f"({it0} + {s})"
-            if s:
+            if s and not fast:
                 self.emit(f"if ({it} >= {n.expr}) break;")
-            deep = (S - 2) * ops
-            if deep:
+            # with prefetching, iteration it+1 must also have landed: its first
+            # k-step is read before the next barrier
+            deep = (S - 3 if plr else S - 2) * ops
+            if deep and fast:
+                self.emit(f"newt::wait_vmcnt<{deep}>();")
+            elif deep:
                 self.emit(f"if ({it} + {S - 2} < {n.expr}) newt::wait_vmcnt<{deep}>(); "
                           f"else newt::wait_vmcnt<0>();")
             else:
@@ -273,7 +482,7 @@ class DotPipeline:
             # issue iteration it+S-1 into the stage that iteration it-1 read
             self.locals[kname] = self.new_scalar(idt, f"({lo_e} + ({it} + {S - 1}) * {stv})")
             self.visit_body(slice_stmts)
-            self.pipe_issue(state, (s + S - 1) % S, f"({it} + {S - 1} < {n.expr})")
+            self.pipe_issue(state, (s + S - 1) % S, f"({it} + {S - 1} < {n.expr})", fast=fast)
             self.visit_body(advance)
             for t in temps:
                 self.locals.pop(t, None)
@@ -281,17 +490,20 @@ class DotPipeline:
             self.locals[kname] = self.new_scalar(idt, f"({lo_e} + {it} * {stv})")
             for nm, r in state["recs"].items():
                 self.locals[nm] = Staged(r, s)
+            state["pf_d"] = 0
+            state["sched"] = None
             self.visit_body([x for i, x in enumerate(flat) if i not in skip])
             for t in temps:
                 self.locals.pop(t, None)
+            if plr:
+                self._plr_fill(state, (s + 1) % S)
+            if fast and state["simple"] and os.environ.get("NEWT_SCHED", "1") != "0":
+                self._sched_hints(state)
         self.pipe_active = None
         self.flush_loads()
         self.loop_backedge(node)
         self.loop_depth -= 1
         self.indent -= 1
-        self.emit("}")
-        self._exit_compound(rec)
-        self.after_loop(node)
 
     def _no_pipe(self, state):
         self.new_hints[("nopipe", state["node"].lineno)] = True
@@ -369,7 +581,7 @@ class DotPipeline:
             names.append(nm)
         state.update(recs=recs, ops=ops, names=names)
 
-    def pipe_issue(self, state, slot, valid):
+    def pipe_issue(self, state, slot, valid, fast=False):
         if state["recs"] is None:
             self._init_recs(state)
         base = state["names"][slot]
@@ -386,7 +598,11 @@ class DotPipeline:
             dt, R, K, fmt = r["dt"], r["R"], r["K"], r["fmt"]
             tile = f"(({dt.ctype}*)({base} + {r['off']}))"
             full = self.mask_all_true(X.mask, X.shape) if r["dma"] else None
-            if r["dma"] and full is not None:
+            if r["dma"] and full is not None and fast:
+                self._dma_stage(V, base, r["off"], fmt, R, K, dt)
+            elif fast:
+                self._reg_stage(V, tile, fmt, R, K, dt)
+            elif r["dma"] and full is not None:
                 cond = valid if full == "true" else f"{valid} && ({full})"
                 # the in-bounds copy is the hot path; the hint moves the masked
                 # register path out of the loop's straight-line code
@@ -601,12 +817,12 @@ class DotPipeline:
                           f"{X.rec['off']});")
                 tiles[idx] = nm
 
-        def frag(idx, i, ks):
+        def frag(idx, i, ks, tile=None, r0=None):
             kind, X = srcs[idx]
             kk = ks * KI
             if kind == "lds":
-                rec, tile = X.rec, tiles[idx]
-                r0 = f"{'_ra' if idx == 0 else '_rb'} + {i * MI}"
+                rec, tile = X.rec, tile or tiles[idx]
+                r0 = r0 or f"{'_ra' if idx == 0 else '_rb'} + {i * MI}"
                 if rec["fmt"] == "k":
                     fn, targs = (("lds_frag_k_perm32", f"{T}, {rec['K']}") if perm else
                                  ("lds_frag_k", f"{T}, {rec['K']}, {MI}"))
@@ -621,11 +837,41 @@ class DotPipeline:
                 slots = [self._slot_for(X.layout, {0: i * MI, 1: kk + e}) for e in range(8)]
             return f"newt::pack8<{T}>({', '.join(X.at(s) for s in slots)})"
 
+        plr = state.get("plr")
+        pf = {}
+        if plr:
+            d = state["pf_d"]
+            state["pf_d"] += 1
+            woff = {0: f"((_wave & {wm - 1}) * {M // wm})",
+                    1: f"(((_wave >> {lo.log2i(wm)}) & {wn - 1}) * {N // wn})"}
+            frags = []
+            for idx, cnt, tag in ((0, RM, "a"), (1, RN, "b")):
+                kind, X = srcs[idx]
+                if kind != "lds":
+                    continue
+                for i in range(cnt):
+                    var = f"_pf{d}{tag}{i}"
+
+                    def fn(slot, idx=idx, i=i, X=X):
+                        tile = f"((const {T}*)({state['names'][slot]} + {X.rec['off']}))"
+                        return frag(idx, i, 0, tile=tile, r0=f"{woff[idx]} + {i * MI}")
+                    frags.append((var, fn))
+                    pf[(idx, i)] = var
+            state["pf"][d] = frags
+
+        def n_reads(idx):
+            kind, X = srcs[idx]
+            if kind != "lds":
+                return 0
+            return 1 if (X.rec["fmt"] == "k" and not perm) else 2
+
         def emit_frags(ks):
             for i in range(RM):
-                self.emit(f"const i16x8 _fa{ks}_{i} = {frag(0, i, ks)};")
+                src = pf.get((0, i)) if ks == 0 else None
+                self.emit(f"const i16x8 _fa{ks}_{i} = {src or frag(0, i, ks)};")
             for j in range(RN):
-                self.emit(f"const i16x8 _fb{ks}_{j} = {frag(1, j, ks)};")
+                src = pf.get((1, j)) if ks == 0 else None
+                self.emit(f"const i16x8 _fb{ks}_{j} = {src or frag(1, j, ks)};")
 
         emit_frags(0)
         for ks in range(nks):
@@ -638,6 +884,8 @@ class DotPipeline:
                     x, y = (fb_, fa_) if orient == "row" else (fa_, fb_)
                     v = f"{accv.var}[{j + RN * i}]"
                     self.emit(f"{v} = newt::mfma_{instr}({x}, {y}, {v});")
+        per_ks = RM * n_reads(0) + RN * n_reads(1)
+        state["sched"] = {"reads": [per_ks] * nks, "mfmas": [RM * RN] * nks}
         self.indent -= 1
         self.emit("}")
         return accv

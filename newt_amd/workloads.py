@@ -139,10 +139,12 @@ def matmul_kernel(a_ptr, b_ptr, c_ptr, M, N, K,
 
 # gfx950 search space: 64-wide waves, 160 KB LDS per CU, 256 CUs. The k-loop is
 # software-pipelined num_stages deep through distinct LDS stages, so tiles of
-# 256x256 with BLOCK_K=32 and 4 stages (128 KB) give each CU one 8-wave
-# workgroup with a 128x64 MFMA sub-tile per wave; smaller tiles keep grids of
-# >= 256 workgroups for smaller problems.
+# 256x256 with BLOCK_K=32 and 4 stages (128 KB) give each CU one workgroup:
+# 4 waves with a 128x128 MFMA sub-tile each (accumulators in AGPRs; half the
+# LDS operand reads per flop of 8 waves) or 8 waves with 128x64; smaller tiles
+# keep grids of >= 256 workgroups for smaller problems.
 MATMUL_CONFIGS = [
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=4, num_stages=4),
     newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=8, num_stages=4),
     newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 64}, num_warps=8, num_stages=2),
     newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=8, num_stages=3),

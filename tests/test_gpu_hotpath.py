@@ -119,7 +119,7 @@ def test_matmul(W, dtype, M, N, K, cfg):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", [(512, 512, 512), (300, 200, 100), (256, 256, 64),
                                    (1024, 768, 1056), (64, 96, 32), (520, 264, 136)])
-@pytest.mark.parametrize("cfg", [(256, 256, 32, 8, 4), (128, 128, 32, 4, 3), (64, 64, 32, 4, 4),
+@pytest.mark.parametrize("cfg", [(256, 256, 32, 8, 4), (256, 256, 32, 4, 4), (128, 128, 32, 4, 3), (64, 64, 32, 4, 4),
                                  (128, 256, 64, 8, 2)])
 def test_matmul_pipelined(W, dtype, M, N, K, cfg):
     """The software-pipelined k-loop (direct-to-LDS stages, ragged fallbacks,
