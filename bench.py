@@ -10,7 +10,8 @@ steps (2*M*N*K flop per step). The one JSON line also carries:
 
   roofline      the matmul kernel vs MI355X's dense fp16 MFMA peak (2.5 PFLOP/s):
                 2*M*N*K flop per launch / the average launch duration from HIP
-                events recorded around each launch on the launch stream
+                events (without system-scope fences) recorded around each
+                launch on the launch stream
   cpu_baseline  the reference's oracle (torch CPU eager, A.float() @ B.float())
                 timed on this host's cores on the same 4096^3 problem
   secondary     vector add / softmax / layernorm (GB/s vs 8 TB/s HBM), bf16
@@ -49,7 +50,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -67,21 +68,65 @@ def seeded(shape, seed, scale=1.0, mean=0.0, dtype=None):
     return t.to(dtype or torch.float32).to("cuda")
 
 
+class _HipEvents:
+    """HIP events on the launch stream, created with hipEventDisableSystemFence:
+    an event record then adds no system-scope cache release between launches
+    (torch's events do, which puts a few microseconds between back-to-back
+    kernels)."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self):
+        import ctypes
+        self.ct = ctypes
+        self.lib = ctypes.CDLL("libamdhip64.so")
+
+    def make(self, n):
+        out = []
+        for _ in range(n):
+            e = self.ct.c_void_p()
+            rc = self.lib.hipEventCreateWithFlags(self.ct.byref(e), self.ct.c_uint(self.DISABLE_SYSTEM_FENCE))
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+            out.append(e)
+        return out
+
+    def record(self, e, stream):
+        rc = self.lib.hipEventRecord(e, self.ct.c_void_p(stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def ms(self, e0, e1):
+        v = self.ct.c_float()
+        rc = self.lib.hipEventElapsedTime(self.ct.byref(v), e0, e1)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return v.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.lib.hipEventDestroy(e)
+
+
 def timed_launches(fn, steps):
     """Run fn() `steps` times back to back on the current stream (where newt
-    launches). Returns (total ms between the first start and last end event,
-    average ms of the per-launch event pairs)."""
+    launches), with a HIP event pair around each launch. Returns (total ms
+    between the first start and last end event, average ms of the per-launch
+    event pairs)."""
     import torch
-    st = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    en = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    hev = _HipEvents()
+    stream = torch.cuda.current_stream().cuda_stream
+    st, en = hev.make(steps), hev.make(steps)
     torch.cuda.synchronize()
     for i in range(steps):
-        st[i].record()
+        hev.record(st[i], stream)
         fn()
-        en[i].record()
+        hev.record(en[i], stream)
     torch.cuda.synchronize()
-    per = [s.elapsed_time(e) for s, e in zip(st, en)]
-    return st[0].elapsed_time(en[-1]), sum(per) / len(per)
+    per = [hev.ms(s, e) for s, e in zip(st, en)]
+    total = hev.ms(st[0], en[-1])
+    hev.destroy(st + en)
+    return total, sum(per) / len(per)
 
 
 def cpu_baseline(S, budget_s):

@@ -711,7 +711,13 @@ class Codegen(ast.NodeVisitor):
             return
         if not isinstance(tgt, ast.Name):
             self.err(node, "can only assign to plain names")
-        self.bind(node, tgt.id, self.visit_expr(node.value))
+        v = self.visit_expr(node.value)
+        if getattr(node, "_newt_prefetch", False) and isinstance(v, LazyLoad) and not self.loop_depth:
+            # a load moved ahead of independent work: issue it here, after the
+            # loads that precede it in the program
+            self.flush_loads()
+            self.materialize_load(v)
+        self.bind(node, tgt.id, v)
 
     def visit_AnnAssign(self, node):
         if node.value is None:

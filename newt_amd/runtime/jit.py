@@ -29,6 +29,11 @@ from ..compiler.codegen import _CKEYWORDS
 from . import hip as _hip
 
 
+# environment switches that change generated code (part of the specialization key)
+_CODEGEN_ENV = ("NEWT_VEC", "NEWT_PIPELINE_DOT", "NEWT_LDS_DMA", "NEWT_MFMA", "NEWT_PID_REMAP",
+                "NEWT_PIPE_VERSION", "NEWT_PLR", "NEWT_SCHED", "NEWT_HOIST_LOADS")
+
+
 def _cache_dir():
     d = os.environ.get("NEWT_CACHE_DIR") or os.path.join(os.path.expanduser("~"), ".newt", "cache")
     os.makedirs(d, exist_ok=True)
@@ -220,9 +225,7 @@ class JITFunction:
 
     @staticmethod
     def _key(constexprs, types, num_warps, num_stages):
-        env = tuple(os.environ.get(k, "") for k in ("NEWT_VEC", "NEWT_PIPELINE_DOT",
-                                                    "NEWT_LDS_DMA", "NEWT_MFMA",
-                                                    "NEWT_PID_REMAP"))
+        env = tuple(os.environ.get(k, "") for k in _CODEGEN_ENV)
         return (tuple(sorted((k, repr(v)) for k, v in constexprs.items())),
                 tuple((n, t.name, s) for n, (t, s) in types.items()),
                 num_warps, num_stages, env)

@@ -224,3 +224,36 @@ def test_lds_budget_check():
     with pytest.raises(CompileError, match="LDS"):
         compile_source(k, {"a_ptr": (F32P, A16), "b_ptr": (F32P, A16), "c_ptr": (F32P, A16)},
                        {"BM": 256, "BN": 256, "BK": 128}, num_warps=8)
+
+
+def test_independent_loads_issue_before_reductions(monkeypatch):
+    """With NEWT_HOIST_LOADS=1, layernorm's weight and bias loads (which do not
+    depend on the row statistics) are issued before the first cross-wave
+    reduction, after the row load."""
+    monkeypatch.setenv("NEWT_HOIST_LOADS", "1")
+    src, _ = compile_source(W.layernorm_kernel, {
+        "x_ptr": (F16P, {"aligned16": True}), "w_ptr": (F16P, {"aligned16": True}),
+        "b_ptr": (F16P, {"aligned16": True}), "out_ptr": (F16P, {"aligned16": True}),
+        "mean_ptr": tp.pointer_type(tp.float32), "rstd_ptr": tp.pointer_type(tp.float32),
+        "N": tp.int32, "stride": tp.int32, "eps": tp.float32}, {"BLOCK_N": 8192})
+    first_reduce = src.index("lane_reduce")
+    xs, ws, bs = (src.index(f"({p} + ") if p != "x" else src.index("load_vec<_Float16, 8>((_p")
+                  for p in ("x", "w_ptr", "b_ptr"))
+    assert xs < ws < bs < first_reduce
+
+
+def test_loads_do_not_move_across_stores():
+    from newt_amd.compiler import hoist_loads
+
+    def k(x_ptr, y_ptr, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        a = nl.load(x_ptr + offs)
+        nl.store(x_ptr + offs, a * 2.0)
+        s = nl.sum(a, axis=0)
+        b = nl.load(x_ptr + offs)
+        nl.store(y_ptr + offs, b + s)
+
+    fndef, _ = fndef_of(k)
+    order = [ast.unparse(st).split(" =")[0].split("(")[0] for st in hoist_loads(fndef).body]
+    # b may pass the reduction but not the store before it
+    assert order == ["offs", "a", "nl.store", "b", "s", "nl.store"]
