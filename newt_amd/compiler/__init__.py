@@ -116,10 +116,12 @@ def hoist_loads(fndef):
 
 
 def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, num_stages=3,
-               max_passes=10):
+               max_passes=10, waves_per_eu=0):
     """Compile a kernel. Returns (hip_source, lds_bytes).
 
     params: list of (name, Param) for the runtime parameters in signature order.
+    waves_per_eu: 0, or the number of waves per SIMD the register allocation
+    must allow (an occupancy request, as Triton's ROCm backend takes it).
     Mirrors the reference boundary compile_fn(...) -> (source, smem)
     (newt/compiler/codegen.py:2758-2765); layout hints learned by one pass are
     fed to the next until no new hint appears."""
@@ -133,7 +135,7 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
     last = None
     for _ in range(max_passes):
         cg = Compiler(fndef, fn_globals, params, constexprs, num_warps, kernel_name,
-                      num_stages=num_stages, hints=hints)
+                      num_stages=num_stages, hints=hints, waves_per_eu=waves_per_eu)
         cg.prefer_rows = prefer_rows
         try:
             src = cg.compile()

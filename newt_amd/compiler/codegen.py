@@ -54,7 +54,10 @@ _CMP = {ast.Eq: "==", ast.NotEq: "!=", ast.Lt: "<", ast.LtE: "<=", ast.Gt: ">",
         ast.GtE: ">="}
 
 _MATH = {  # name -> (fp32 fn, fp64 fn)
-    "exp": ("expf", "exp"), "exp2": ("exp2f", "exp2"), "log": ("logf", "log"),
+    # fp32 exp2 is the hardware v_exp_f32 (1 ulp); results below 2**-126 flush
+    # to zero instead of taking the library's denormal-scaling path, which
+    # would cost a compare, two selects and an ldexp per element
+    "exp": ("expf", "exp"), "exp2": ("__builtin_amdgcn_exp2f", "exp2"), "log": ("logf", "log"),
     "log2": ("log2f", "log2"), "sqrt": ("sqrtf", "sqrt"), "rsqrt": ("rsqrtf", "rsqrt"),
     "sin": ("sinf", "sin"), "cos": ("cosf", "cos"), "tanh": ("tanhf", "tanh"),
     "erf": ("erff", "erf"), "floor": ("floorf", "floor"), "ceil": ("ceilf", "ceil"),
@@ -122,7 +125,7 @@ class _Prepass:
 
 class Codegen(ast.NodeVisitor):
     def __init__(self, fndef, fn_globals, params, constexprs, num_warps, kernel_name,
-                 num_stages=3, hints=None):
+                 num_stages=3, hints=None, waves_per_eu=0):
         """params: list of (name, Param) for runtime parameters in signature order."""
         self.fndef = fndef
         self.globals = fn_globals
@@ -130,6 +133,7 @@ class Codegen(ast.NodeVisitor):
         self.T = 64 * num_warps
         self.name = kernel_name
         self.num_stages = num_stages
+        self.waves_per_eu = waves_per_eu
         self.hints = dict(hints or {})
         self.new_hints = {}
         self.lines = []
@@ -674,7 +678,11 @@ class Codegen(ast.NodeVisitor):
             out.append(f"#define {nm} {off}")
         out.append(f"#define _LDSA {arena_off}")
         out.append("")
-        out.append(f'extern "C" __global__ void __launch_bounds__({self.T}) '
+        # waves_per_eu > 0 asks for that many waves per SIMD: the register
+        # allocator then keeps each wave within 512 / waves_per_eu registers
+        occ = (f"__attribute__((amdgpu_waves_per_eu({self.waves_per_eu}))) "
+               if self.waves_per_eu else "")
+        out.append(f'extern "C" __global__ void __launch_bounds__({self.T}) {occ}'
                    f'{self.name}({", ".join(sig)}) {{')
         if lds_total:
             out.append(f"  __shared__ __attribute__((aligned(16))) unsigned char _lds[{lds_total}];")

@@ -8,12 +8,14 @@ over META (runtime args + constexprs + num_warps); an empty grid is a no-op;
 launches go on torch's current stream and nothing is synchronized.
 
 What differs is the backend: `num_warps` counts wave64s (64 threads each, so at
-most 16); kernels are specialized, as Triton does, on integer arguments equal
-to 1 and on the power-of-two divisibility (up to 16) of integers and of
-pointer addresses; code objects come from hipRTC and are cached on disk under
-~/.newt/cache (NEWT_CACHE_DIR) keyed by the HIP source, the device-template
-header, the target, the hipRTC version and this backend's version; launches pass
-one packed argument buffer through hipModuleLaunchKernel.
+most 16); an optional `waves_per_eu=N` launch option (as in Triton's ROCm
+backend) asks the register allocator to leave room for N waves per SIMD;
+kernels are specialized, as Triton does, on integer arguments equal to 1 and on
+the power-of-two divisibility (up to 16) of integers and of pointer addresses;
+code objects come from hipRTC and are cached on disk under ~/.newt/cache
+(NEWT_CACHE_DIR) keyed by the HIP source, the device-template header, the
+target, the hipRTC version and this backend's version; launches pass one packed
+argument buffer through hipModuleLaunchKernel.
 """
 
 import ast
@@ -192,7 +194,7 @@ class JITFunction:
             return tp.float32, ""
         raise TypeError(f"unsupported kernel argument type {type(val)} for '{name}'")
 
-    def _compile(self, key, constexprs, runtime_types, num_warps, num_stages):
+    def _compile(self, key, constexprs, runtime_types, num_warps, num_stages, waves_per_eu=0):
         params = []
         for name in self.param_names:
             if name in self.constexpr_names:
@@ -205,36 +207,40 @@ class JITFunction:
         khash = hashlib.sha256(repr(key).encode()).hexdigest()[:8]
         kname = f"{self.fn.__name__}_{khash}"
         source, lds = compile_fn(self.fndef, self.fn.__globals__, params, constexprs,
-                                 num_warps, kname, num_stages=num_stages)
+                                 num_warps, kname, num_stages=num_stages,
+                                 waves_per_eu=waves_per_eu)
         if os.environ.get("NEWT_DEBUG"):
             print(f"=== newt: {kname} (lds={lds}b, waves={num_warps}) ===")
             print(source)
         return CompiledKernel(kname, source, lds, num_warps, params)
 
-    def specialize(self, *args, num_warps=4, num_stages=3, **kwargs):
+    def specialize(self, *args, num_warps=4, num_stages=3, waves_per_eu=0, **kwargs):
         """Compile (without launching) for these arguments; returns the
         CompiledKernel (source, code object, resource usage)."""
         constexprs, runtime = self._classify(args, kwargs)
         types = {n: self._type_of(n, v) for n, v in runtime.items()}
-        key = self._key(constexprs, types, num_warps, num_stages)
+        key = self._key(constexprs, types, num_warps, num_stages, waves_per_eu)
         ck = self.cache.get(key)
         if ck is None:
-            ck = self._compile(key, constexprs, types, num_warps, num_stages)
+            ck = self._compile(key, constexprs, types, num_warps, num_stages, waves_per_eu)
             self.cache[key] = ck
         return ck
 
     @staticmethod
-    def _key(constexprs, types, num_warps, num_stages):
+    def _key(constexprs, types, num_warps, num_stages, waves_per_eu=0):
         env = tuple(os.environ.get(k, "") for k in _CODEGEN_ENV)
         return (tuple(sorted((k, repr(v)) for k, v in constexprs.items())),
                 tuple((n, t.name, s) for n, (t, s) in types.items()),
-                num_warps, num_stages, env)
+                num_warps, num_stages, waves_per_eu, env)
 
     def _run(self, grid, *args, **kwargs):
         import torch
 
         num_warps = kwargs.pop("num_warps", 4)
         num_stages = kwargs.pop("num_stages", 3)
+        waves_per_eu = int(kwargs.pop("waves_per_eu", 0))
+        if not 0 <= waves_per_eu <= 8:
+            raise ValueError(f"waves_per_eu must be in 0..8 (0 = no request), got {waves_per_eu}")
         if num_warps not in (1, 2, 4, 8, 16):
             raise ValueError(f"num_warps must be a power of two <= 16 (wave64s per "
                              f"workgroup, at most 1024 threads), got {num_warps}")
@@ -242,10 +248,10 @@ class JITFunction:
             raise ValueError(f"num_stages must be in 1..8, got {num_stages}")
         constexprs, runtime = self._classify(args, kwargs)
         types = {n: self._type_of(n, v) for n, v in runtime.items()}
-        key = self._key(constexprs, types, num_warps, num_stages)
+        key = self._key(constexprs, types, num_warps, num_stages, waves_per_eu)
         ck = self.cache.get(key)
         if ck is None:
-            ck = self._compile(key, constexprs, types, num_warps, num_stages)
+            ck = self._compile(key, constexprs, types, num_warps, num_stages, waves_per_eu)
             self.cache[key] = ck
         values = []
         dev = None

@@ -14,7 +14,9 @@ reference's examples/01-05), extended to the BASELINE configurations:
                     to the diagonal, p cast to V's dtype before P @ V, and the
                     softmax written on exp2 with log2(e) folded into the scale
                     (exp(x) = exp2(x*log2 e): the same softmax, fewer
-                    instructions per element)
+                    instructions per element); launched with waves_per_eu=2 so
+                    two waves share each SIMD and one wave's softmax runs while
+                    the other's MFMAs do
 Everything is compiled by newt_amd's compiler to HIP for gfx950.
 """
 
@@ -229,7 +231,7 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
 
 
 def attention(q, k, v, causal=False, scale=None, out=None, BLOCK_M=128, BLOCK_N=64,
-              num_warps=4, num_stages=2):
+              num_warps=4, num_stages=2, waves_per_eu=2):
     B, H, S, D = q.shape
     out = torch.empty_like(q) if out is None else out
     scale = D ** -0.5 if scale is None else scale
@@ -240,5 +242,6 @@ def attention(q, k, v, causal=False, scale=None, out=None, BLOCK_M=128, BLOCK_N=
                            v.stride(0), v.stride(1), v.stride(2),
                            out.stride(0), out.stride(1), out.stride(2),
                            BLOCK_M=BLOCK_M, BLOCK_N=BLOCK_N, D=D, CAUSAL=causal,
-                           num_warps=num_warps, num_stages=num_stages)
+                           num_warps=num_warps, num_stages=num_stages,
+                           waves_per_eu=waves_per_eu)
     return out
