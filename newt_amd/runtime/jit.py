@@ -34,6 +34,16 @@ from . import hip as _hip
 # environment switches that change generated code (part of the specialization key)
 _CODEGEN_ENV = ("NEWT_VEC", "NEWT_PIPELINE_DOT", "NEWT_LDS_DMA", "NEWT_MFMA", "NEWT_PID_REMAP",
                 "NEWT_PIPE_VERSION", "NEWT_PLR", "NEWT_SCHED", "NEWT_HOIST_LOADS")
+_CODEGEN_ENV_B = tuple(k.encode() for k in _CODEGEN_ENV)
+
+
+def _env_snapshot():
+    """The codegen switches as a tuple, read without os.environ's per-key
+    string encoding (a launch reads it on every call)."""
+    data = getattr(os.environ, "_data", None)
+    if isinstance(data, dict):
+        return tuple(map(data.get, _CODEGEN_ENV_B))
+    return tuple(os.environ.get(k) for k in _CODEGEN_ENV)
 
 
 def _cache_dir():
@@ -139,6 +149,9 @@ class JITFunction:
         self.defaults = {n: p.default for n, p in sig.parameters.items()
                          if p.default is not inspect.Parameter.empty}
         self.cache = {}
+        # launch fast path: call signature -> (CompiledKernel, argument plan)
+        self._fast = {}
+        self._cx_pos = tuple(n in self.constexpr_names for n in self.param_names)
 
     def __getitem__(self, grid):
         return functools.partial(self._run, grid)
@@ -233,6 +246,38 @@ class JITFunction:
                 tuple((n, t.name, s) for n, (t, s) in types.items()),
                 num_warps, num_stages, waves_per_eu, env)
 
+    def _call_signature(self, args, kwargs, opts):
+        """A cheap, hashable summary of everything a launch specializes on:
+        per argument its kind, dtype, 16-byte alignment, device, int32 range,
+        ==1 and power-of-two divisibility (the value itself for constexprs),
+        plus the launch options and the codegen switches. Raises TypeError for
+        an unhashable constexpr value."""
+        import torch
+
+        cx = self._cx_pos
+        out = [opts, _env_snapshot()]
+        for i, v in enumerate(args):
+            out.append(("C", type(v), v) if i < len(cx) and cx[i] else _arg_sig(v, torch))
+        for k, v in kwargs.items():
+            out.append((k, ("C", type(v), v) if k in self.constexpr_names else _arg_sig(v, torch)))
+        sig = tuple(out)
+        hash(sig)
+        return sig
+
+    def _plan(self, ck, args, kwargs):
+        """Where each kernel parameter's value comes from on a fast launch."""
+        pos = {n: i for i, n in enumerate(self.param_names[:len(args)])}
+        plan = []
+        for name, p in ck.params:
+            kind = 0 if isinstance(p.dtype, tp.pointer_type) else (1 if p.dtype == tp.float32 else 2)
+            if name in pos:
+                plan.append((0, pos[name], kind))
+            elif name in kwargs:
+                plan.append((1, name, kind))
+            else:
+                plan.append((2, self.defaults[name], kind))
+        return ck, tuple(plan)
+
     def _run(self, grid, *args, **kwargs):
         import torch
 
@@ -246,33 +291,43 @@ class JITFunction:
                              f"workgroup, at most 1024 threads), got {num_warps}")
         if not 1 <= num_stages <= 8:
             raise ValueError(f"num_stages must be in 1..8, got {num_stages}")
-        constexprs, runtime = self._classify(args, kwargs)
-        types = {n: self._type_of(n, v) for n, v in runtime.items()}
-        key = self._key(constexprs, types, num_warps, num_stages, waves_per_eu)
-        ck = self.cache.get(key)
-        if ck is None:
-            ck = self._compile(key, constexprs, types, num_warps, num_stages, waves_per_eu)
-            self.cache[key] = ck
+        try:
+            csig = self._call_signature(args, kwargs, (num_warps, num_stages, waves_per_eu))
+        except TypeError:
+            csig = None
+        fast = self._fast.get(csig) if csig is not None else None
+        if fast is None:
+            constexprs, runtime = self._classify(args, kwargs)
+            types = {n: self._type_of(n, v) for n, v in runtime.items()}
+            key = self._key(constexprs, types, num_warps, num_stages, waves_per_eu)
+            ck = self.cache.get(key)
+            if ck is None:
+                ck = self._compile(key, constexprs, types, num_warps, num_stages, waves_per_eu)
+                self.cache[key] = ck
+            fast = self._plan(ck, args, kwargs)
+            if csig is not None:
+                self._fast[csig] = fast
+        ck, plan = fast
         values = []
         dev = None
-        for name in ck.param_names:
-            v = runtime[name]
-            t = types[name][0]
-            if isinstance(t, tp.pointer_type):
+        for src, ref, kind in plan:
+            v = args[ref] if src == 0 else (kwargs[ref] if src == 1 else ref)
+            if kind == 0:
                 if dev is None:
                     dev = torch.cuda.current_device()
                 if v.device.index not in (None, dev):
                     raise ValueError(
-                        f"tensor '{name}' is on {v.device} but the current device is "
+                        f"tensor is on {v.device} but the current device is "
                         f"cuda:{dev}; newt launches on the current device")
                 values.append(v.data_ptr())
-            elif t == tp.float32:
+            elif kind == 1:
                 values.append(float(v))
             else:
                 values.append(v)
         if callable(grid):
-            meta = dict(runtime)
-            meta.update(constexprs)
+            meta = dict(self.defaults)
+            meta.update(zip(self.param_names, args))
+            meta.update(kwargs)
             meta["num_warps"] = num_warps
             g = grid(meta)
         else:
@@ -284,6 +339,19 @@ class JITFunction:
             return  # empty grid: no-op
         stream = torch.cuda.current_stream().cuda_stream
         ck.launch(g, values, stream)
+
+
+def _arg_sig(v, torch):
+    t = type(v)
+    if t is int:
+        return ("i", v == 1, _pow2_div(v), -(2 ** 31) <= v < 2 ** 31)
+    if t is float:
+        return "f"
+    if t is bool:
+        return "b"
+    if isinstance(v, torch.Tensor):
+        return (v.dtype, v.data_ptr() % 16 == 0, v.device)
+    return ("?", t, v)
 
 
 def jit(fn=None):

@@ -163,3 +163,27 @@ def test_constexpr_host_arithmetic():
     assert int(c) == 64
     assert c == 64
     assert c + 1 == 65 and c // 2 == 32 and 100 - c == 36
+
+
+def test_launch_fast_path_tracks_specialization(monkeypatch):
+    """The launch fast path is keyed on everything the slow path specializes
+    on: a call differing in an int's ==1 / divisibility, a constexpr value, a
+    launch option or a codegen switch must not reuse another call's kernel."""
+    import newt_amd.runtime.jit as J
+
+    @newt.jit
+    def k(x_ptr, n, BLOCK: nl.constexpr):
+        nl.store(x_ptr + nl.arange(0, BLOCK), 1.0, mask=nl.arange(0, BLOCK) < n)
+
+    x = torch.zeros(64)
+    sig = lambda *a, **kw: k._call_signature(a, kw, (4, 3, 0))
+    base = sig(x, 64, BLOCK=64)
+    assert sig(x, 64, BLOCK=64) == base
+    assert sig(x, 1, BLOCK=64) != base           # n == 1 specializes
+    assert sig(x, 48, BLOCK=64) == base          # both divisible by 16: same kernel
+    assert sig(x, 24, BLOCK=64) != base          # divisible by 8 only
+    assert sig(x, 64, BLOCK=128) != base         # constexpr value
+    assert sig(x, 1 << 40, BLOCK=64) != base     # int64 argument
+    assert k._call_signature((x, 64), {"BLOCK": 64}, (8, 3, 0)) != base
+    monkeypatch.setenv("NEWT_PID_REMAP", "0")
+    assert sig(x, 64, BLOCK=64) != base
