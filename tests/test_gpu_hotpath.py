@@ -156,6 +156,19 @@ def test_attention(W, causal, B, H, S, D):
     assert orc.rel_frobenius(npf(o), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,S,D", [(1, 2, 256, 128), (2, 2, 300, 128), (1, 1, 1000, 128),
+                                     (1, 2, 64, 128)])
+def test_attention_default_config(W, causal, B, H, S, D):
+    """The configuration bench.py and users get (BLOCK_M=128, BLOCK_N=64, 4
+    waves, 2 stages, waves_per_eu=2), including ragged sequence lengths."""
+    q, k, v = (seeded((B, H, S, D), s, dtype=torch.bfloat16) for s in (16, 17, 18))
+    o = W.attention(q, k, v, causal=causal)
+    ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    assert orc.rel_frobenius(npf(o), ref) <= 1e-2
+
+
 def test_attention_golden(W):
     for causal in (False, True):
         g = np.load(f"tests/golden/attention_1x2x64x32_{'causal' if causal else 'full'}.npz")
