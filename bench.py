@@ -36,6 +36,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA, published
 PEAK_GBS = 8000.0      # MI355X HBM3E, published
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA, published
 METRIC = "fp16 4096^3 matmul TFLOP/s (% MFMA peak); softmax/layernorm GB/s (% HBM)"
 # HBM bytes per matmul launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on
 # this command, scaled by the copy-kernel calibration (see profiles/)
@@ -335,16 +336,30 @@ def secondary():
                 res.append({"workload": name, "value": round(v, 1), "unit": "GB/s",
                             "ms_flushed": round(ms, 5), "frac_hbm": round(v / PEAK_GBS, 4),
                             "ms_back_to_back": round(kern, 5), "bytes": work})
+        from oracle import newt_oracle as orc
         S = 4096
-        a = seeded((S, S), 4, scale=S ** -0.5, dtype=torch.bfloat16)
-        b = seeded((S, S), 5, scale=S ** -0.5, dtype=torch.bfloat16)
-        c = torch.empty(S, S, device="cuda", dtype=torch.bfloat16)
-        W.matmul(a, b, c)
-        cfg = W.matmul_tuned.best_config
-        _, kern = timed_launches(lambda: W.matmul(a, b, c, config=cfg), 20)
-        v = 2.0 * S ** 3 / (kern * 1e-3) / 1e12
-        res.append({"workload": "matmul bf16 4096^3", "value": round(v, 2), "unit": "TFLOP/s",
-                    "ms": round(kern, 5), "frac_mfma": round(v / PEAK_TFLOPS, 4)})
+        for dt, tuned, peak, name in (
+                (torch.bfloat16, W.matmul_tuned, PEAK_TFLOPS, "matmul bf16 4096^3"),
+                (torch.float32, W.matmul_tuned_fp32, PEAK_FP32_TFLOPS,
+                 "matmul fp32 4096^3 (fp32 MFMA, full precision; the reference runs tf32)")):
+            a = seeded((S, S), 4, scale=S ** -0.5, dtype=dt)
+            b = seeded((S, S), 5, scale=S ** -0.5, dtype=dt)
+            c = torch.empty(S, S, device="cuda", dtype=dt)
+            W.matmul(a, b, c)
+            torch.cuda.synchronize()
+            rows = slice(0, 128)
+            ref = orc.matmul(a[rows].float().cpu().numpy(), b.float().cpu().numpy(),
+                             "bfloat16" if dt == torch.bfloat16 else "float32")
+            err = orc.rel_frobenius(c[rows].float().cpu().numpy(), ref)
+            assert err <= 1e-2, f"{name}: rel. Frobenius {err}"
+            cfg = tuned.best_config
+            _, kern = timed_launches(lambda: W.matmul(a, b, c, config=cfg), 20)
+            v = 2.0 * S ** 3 / (kern * 1e-3) / 1e12
+            res.append({"workload": name, "value": round(v, 2), "unit": "TFLOP/s",
+                        "ms": round(kern, 5), "frac_mfma": round(v / peak, 4),
+                        "rel_frobenius_vs_oracle": err,
+                        "tile": dict(cfg.kwargs), "num_warps": cfg.num_warps,
+                        "num_stages": cfg.num_stages})
     except Exception as e:  # report what was measured, and why the rest was not
         res.append({"error": f"{type(e).__name__}: {str(e)[:300]}"})
     return res

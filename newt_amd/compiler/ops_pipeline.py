@@ -563,7 +563,7 @@ class DotPipeline:
                 self._no_pipe(state)
             fmt = self._tile_format(X, kdim)
             nbytes = self.tile_bytes(R, K, dt)
-            dma = self._dma_ok(V, fmt, R, K, dt)
+            dma = self._dma_ok(V, fmt, R, K, dt) and os.environ.get("NEWT_LDS_DMA", "1") != "0"
             epc = 16 // dt.itemsize
             if dma:
                 ops += R * K // epc // self.T

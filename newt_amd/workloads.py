@@ -159,6 +159,16 @@ MATMUL_CONFIGS = [
 
 matmul_tuned = newt.autotune(configs=MATMUL_CONFIGS, key=["M", "N", "K"])(matmul_kernel)
 
+# fp32 operands run on the fp32 MFMA (v_mfma_f32_32x32x2_f32, full precision;
+# gfx950 has no tf32) with synchronous LDS staging: smaller k-steps, one stage
+MATMUL_CONFIGS_FP32 = [
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 16}, num_warps=8, num_stages=1),
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 16}, num_warps=8, num_stages=1),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 16}, num_warps=4, num_stages=1),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=4, num_stages=1),
+]
+matmul_tuned_fp32 = newt.autotune(configs=MATMUL_CONFIGS_FP32, key=["M", "N", "K"])(matmul_kernel)
+
 
 def matmul(a, b, c=None, config=None):
     M, K = a.shape
@@ -169,7 +179,7 @@ def matmul(a, b, c=None, config=None):
             c.stride(0), c.stride(1))
     if config is None:
         grid = lambda meta: (newt.cdiv(M, meta["BLOCK_M"]), newt.cdiv(N, meta["BLOCK_N"]))
-        matmul_tuned[grid](*args)
+        (matmul_tuned_fp32 if a.dtype == torch.float32 else matmul_tuned)[grid](*args)
     else:
         grid = (newt.cdiv(M, config.kwargs["BLOCK_M"]), newt.cdiv(N, config.kwargs["BLOCK_N"]))
         matmul_kernel[grid](*args, **config.kwargs, num_warps=config.num_warps,
