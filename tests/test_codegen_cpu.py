@@ -30,7 +30,7 @@ def fndef_of(fn):
     return ast.parse(textwrap.dedent(inspect.getsource(fn))).body[0], fn.__globals__
 
 
-def compile_source(fn, arg_types, constexprs, num_warps=4, num_stages=3):
+def compile_source(fn, arg_types, constexprs, num_warps=4, num_stages=3, waves_per_eu=0):
     """Run the code generator directly: (HIP source, LDS bytes)."""
     fndef, glb = fndef_of(fn)
     params = []
@@ -40,7 +40,8 @@ def compile_source(fn, arg_types, constexprs, num_warps=4, num_stages=3):
         else:
             facts = {}
         params.append((n, Param(t, n, **facts)))
-    return compile_fn(fndef, glb, params, constexprs, num_warps, "k", num_stages=num_stages)
+    return compile_fn(fndef, glb, params, constexprs, num_warps, "k", num_stages=num_stages,
+                      waves_per_eu=waves_per_eu)
 
 
 def isa(src):
@@ -141,6 +142,47 @@ def test_attention_compiles_with_mfma():
         assert lds <= 160 * 1024
         asm = isa(src)
         assert "v_mfma_f32_32x32x16_bf16" in asm or "v_mfma_f32_16x16x32_bf16" in asm
+
+
+def _vgprs(src):
+    """Arch + accumulation VGPRs of the gfx950 code object built here."""
+    import os
+    import tempfile
+    from newt_amd.runtime import hip
+    with tempfile.NamedTemporaryFile(suffix=".co", delete=False) as f:
+        f.write(hip.compile_hip(src, "k"))
+        path = f.name
+    try:
+        notes = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--notes", path],
+                               capture_output=True, text=True, check=True).stdout
+    finally:
+        os.unlink(path)
+    return int(re.search(r"\.vgpr_count:\s+(\d+)", notes).group(1))
+
+
+def test_waves_per_eu_caps_registers():
+    """waves_per_eu=2 emits the occupancy attribute and keeps flash attention
+    within 256 registers (two waves per SIMD); without it the kernel uses more."""
+    args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
+    args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})
+    for n in ("sqb", "sqh", "sqm", "skb", "skh", "skn", "svb", "svh", "svn", "sob", "soh", "som"):
+        args[n] = (tp.int32, D16)
+    cx = {"BLOCK_M": 128, "BLOCK_N": 64, "D": 128, "CAUSAL": False}
+    src2, _ = compile_source(W.attention_kernel, args, cx, num_warps=4, num_stages=2,
+                             waves_per_eu=2)
+    src0, _ = compile_source(W.attention_kernel, args, cx, num_warps=4, num_stages=2)
+    assert "amdgpu_waves_per_eu(2)" in src2 and "amdgpu_waves_per_eu" not in src0
+    assert _vgprs(src2) <= 256 < _vgprs(src0)
+
+
+def test_exp2_is_the_hardware_instruction():
+    def k(x_ptr, o_ptr, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        nl.store(o_ptr + offs, nl.exp2(nl.load(x_ptr + offs)))
+
+    src, _ = compile_source(k, {"x_ptr": F32P, "o_ptr": F32P}, {"BLOCK": 1024})
+    asm = isa(src)
+    assert "v_exp_f32" in asm and "v_ldexp" not in asm
 
 
 def test_constexpr_branch_pruning():
