@@ -360,6 +360,25 @@ def secondary():
                         "rel_frobenius_vs_oracle": err,
                         "tile": dict(cfg.kwargs), "num_warps": cfg.num_warps,
                         "num_stages": cfg.num_stages})
+        # deuteron: the same matmul written as tiles, traced to newt and
+        # autotuned against its eager oracle (examples/deuteron/01_matmul.py)
+        import tempfile
+        os.environ["DEUTERON_CACHE_DIR"] = tempfile.mkdtemp(prefix="deuteron-bench-")  # tune here
+        k = W.dt_matmul
+        a = seeded((S, S), 4, scale=S ** -0.5, dtype=torch.float16)
+        b = seeded((S, S), 5, scale=S ** -0.5, dtype=torch.float16)
+        c = torch.empty(S, S, device="cuda", dtype=torch.float16)
+        k(a, b, c)
+        torch.cuda.synchronize()
+        ref = orc.matmul(a[:128].float().cpu().numpy(), b.float().cpu().numpy(), "float16")
+        err = orc.rel_frobenius(c[:128].float().cpu().numpy(), ref)
+        assert err <= 1e-2, f"deuteron matmul: rel. Frobenius {err}"
+        _, kern = timed_launches(lambda: k(a, b, c), 20)
+        v = 2.0 * S ** 3 / (kern * 1e-3) / 1e12
+        res.append({"workload": "deuteron matmul fp16 4096^3 (autotuned tile DSL)",
+                    "value": round(v, 2), "unit": "TFLOP/s", "ms": round(kern, 5),
+                    "frac_mfma": round(v / PEAK_TFLOPS, 4), "rel_frobenius_vs_oracle": err,
+                    "config": dict(k.best_config)})
     except Exception as e:  # report what was measured, and why the rest was not
         res.append({"error": f"{type(e).__name__}: {str(e)[:300]}"})
     return res

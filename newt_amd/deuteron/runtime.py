@@ -14,7 +14,8 @@ Protocol of the reference (deuteron/runtime.py:1-311):
 
 The search space is this backend's: tile sizes that map onto 32x32 MFMA tiles
 for dot kernels, num_warps counted in 64-wide waves, and num_stages for the
-software-pipelined k-loop.
+software-pipelined k-loop. Dot kernels try a few known-good gfx950 tilings
+before the random sample.
 """
 
 import ast
@@ -152,7 +153,9 @@ class Kernel:
 
     # ------------------------------------------------------------ autotuning
     def _key(self, ks, args):
-        h = hashlib.sha256(ks.source.encode()).hexdigest()[:12]
+        h = getattr(ks, "_hash", None)
+        if h is None:
+            h = ks._hash = hashlib.sha256(ks.source.encode()).hexdigest()[:12]
         shapes = tuple(tuple(_pow2(s) for s in a.shape) if torch.is_tensor(a) else None
                        for a in args)
         dts = tuple(str(a.dtype) if torch.is_tensor(a) else "" for a in args)
@@ -192,6 +195,24 @@ class Kernel:
         if dot:
             space["num_stages"] = [2, 3, 4]
         return space
+
+    @staticmethod
+    def _priors(ks, space):
+        """Configurations tried before the random sample for dot kernels: the
+        tiles gfx950 matmuls run best with (256x256 or 128x128 output tiles,
+        k-tiles of 32/64, 4 or 8 waves, 3-4 stages), mapped onto this kernel's
+        grid tiles and inner (k) tiles."""
+        if "num_stages" not in space:
+            return []
+        grid = {td.block for td in ks.grid_tiles}
+        out = []
+        for g, kt, nw, ns in ((256, 32, 4, 4), (256, 32, 8, 4), (128, 64, 4, 3), (128, 32, 4, 4)):
+            cfg = Config(num_warps=nw, num_stages=ns)
+            for nm in ks.tunable:
+                cfg[nm] = g if nm in grid else kt
+            if all(cfg[k] in space[k] for k in space):
+                out.append(cfg)
+        return out
 
     @staticmethod
     def _neighbours(cfg, space):
@@ -247,6 +268,7 @@ class Kernel:
         every = [Config(zip(keys, vals)) for vals in itertools.product(*[space[k] for k in keys])]
         rng = random.Random(0)
         cands = every if len(every) <= self.samples else rng.sample(every, self.samples)
+        cands = self._priors(ks, space) + cands
         seen, results = set(), []
         for cfg in cands:
             sig = frozenset(cfg.items())

@@ -17,6 +17,8 @@ reference's examples/01-05), extended to the BASELINE configurations:
                     instructions per element); launched with waves_per_eu=2 so
                     two waves share each SIMD and one wave's softmax runs while
                     the other's MFMAs do
+  dt_matmul         examples/deuteron/01_matmul.py (unchanged body): the tile
+                    DSL traced to newt and autotuned against its eager oracle
 Everything is compiled by newt_amd's compiler to HIP for gfx950.
 """
 
@@ -255,3 +257,18 @@ def attention(q, k, v, causal=False, scale=None, out=None, BLOCK_M=128, BLOCK_N=
                            num_warps=num_warps, num_stages=num_stages,
                            waves_per_eu=waves_per_eu)
     return out
+
+
+# ---------------------------------------------------------------------------
+# 6. deuteron matmul (examples/deuteron/01_matmul.py, unchanged body)
+# ---------------------------------------------------------------------------
+from . import deuteron as dt  # noqa: E402
+
+
+@dt.kernel
+def dt_matmul(x, y, out):
+    for tile_m, tile_n in dt.tile([x.shape[0], y.shape[1]]):
+        acc = dt.zeros([tile_m, tile_n], dtype=dt.float32)
+        for tile_k in dt.tile(x.shape[1]):
+            acc += x[tile_m, tile_k] @ y[tile_k, tile_n]
+        out[tile_m, tile_n] = acc

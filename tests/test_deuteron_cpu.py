@@ -63,6 +63,17 @@ def test_matmul_source_is_a_pipelineable_dot_loop():
     assert ks.store_params == {"out"}
 
 
+def test_dot_kernels_try_gfx950_priors_first():
+    x, y, o = torch.empty(64, 32).half(), torch.empty(32, 48).half(), torch.empty(64, 48).half()
+    ks = matmul._source_for((x, y, o))
+    pri = matmul._priors(ks, matmul._space(ks))
+    assert dict(pri[0]) == {"num_warps": 4, "num_stages": 4, "BLOCK_TILE_M": 256,
+                            "BLOCK_TILE_N": 256, "BLOCK_TILE_K": 32}
+    xs, os_ = torch.empty(8, 100), torch.empty(8, 100)
+    ks2 = softmax._source_for((xs, os_))
+    assert softmax._priors(ks2, softmax._space(ks2)) == []
+
+
 def test_masks_reach_reductions():
     x = torch.empty(10, 30)
     src = softmax.to_newt_source(x, x)
