@@ -58,7 +58,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--config", default=None, help="BM,BN,BK,warps,stages (skip autotune)")
     ap.add_argument("--only", default=None,
-                    choices=["matmul", "add", "softmax", "layernorm", "attention", "copy"])
+                    help="run one workload for profiler runs: 'matmul', 'copy', or the "
+                         "start of a secondary workload's name (e.g. 'softmax fp32 4096x4096')")
     return ap.parse_args()
 
 
