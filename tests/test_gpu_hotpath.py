@@ -135,6 +135,39 @@ def test_matmul_pipelined(W, dtype, M, N, K, cfg):
     assert orc.rel_frobenius(npf(c), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("ta,tb", [(False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(512, 384, 256), (300, 200, 136), (1024, 1024, 512)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_matmul_transposed_operands(W, dtype, M, N, K, ta, tb):
+    """Column-major A and/or B (transposed views: unit stride along the other
+    dim) take other LDS tile formats and copy paths than row-major inputs."""
+    a = seeded((K, M) if ta else (M, K), 30, scale=K ** -0.5, dtype=dtype)
+    b = seeded((N, K) if tb else (K, N), 31, scale=K ** -0.5, dtype=dtype)
+    a = a.t() if ta else a
+    b = b.t() if tb else b
+    c = W.matmul(a, b)
+    ref = orc.matmul(npf(a), npf(b), "float16" if dtype == torch.float16 else "bfloat16")
+    assert orc.rel_frobenius(npf(c), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("cfg", [(256, 256, 32, 4, 4), (256, 256, 32, 8, 4), (128, 128, 64, 4, 3)])
+def test_matmul_strided_rows(W, cfg):
+    """Row strides larger than the row (views into a wider buffer) and an
+    output written into a strided view."""
+    import newt_amd as newt
+    BM, BN, BK, nw, ns = cfg
+    big_a = seeded((512, 768), 32, scale=0.05, dtype=torch.float16)
+    big_b = seeded((512, 640), 33, scale=0.05, dtype=torch.float16)
+    a, b = big_a[:, 64:576], big_b[:, 32:544]        # [512, 512] each, strides 768 / 640
+    out = torch.zeros(512, 1024, device="cuda", dtype=torch.float16)
+    c = out[:, 256:768]
+    W.matmul(a, b, c, config=newt.Config({"BLOCK_M": BM, "BLOCK_N": BN, "BLOCK_K": BK},
+                                         num_warps=nw, num_stages=ns))
+    ref = orc.matmul(npf(a), npf(b), "float16")
+    assert orc.rel_frobenius(npf(c), ref) <= 1e-2
+    assert not out[:, :256].any() and not out[:, 768:].any()
+
+
 def test_matmul_golden(W):
     import newt_amd as newt
     cfg = newt.Config({"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 32}, num_warps=4, num_stages=2)
