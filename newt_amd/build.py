@@ -6,9 +6,6 @@
     is compiled offline with hipcc for gfx950, instantiating every template the
     code generator emits, so a broken header fails the build instead of the
     first kernel launch.
-  * code objects of the hot-path kernels (the five BASELINE configurations) are
-    produced by the newt compiler + hipRTC here on the CPU and stored in the
-    in-tree code-object cache, so a GPU host starts with a warm cache.
 
 Run: python -m newt_amd.build
 """

@@ -1,7 +1,7 @@
 """The five hot-path workloads written in the newt DSL, with host wrappers.
 
 These are user-level kernels exactly as a newt user writes them (the
-reference's examples/01-05), extended to the BASELINE configurations:
+reference's examples/01-05), extended to the benchmark configurations:
   add_kernel        examples/01_vector_add.py:14-21 (unchanged)
   softmax_kernel    examples/02_fused_softmax.py:15-24 (unchanged)
   layernorm_kernel  examples/03_layernorm.py:13-27 + stores of the saved
