@@ -741,10 +741,9 @@ class DotPipeline:
                 self.locals[na] = self.to_reg(v, L)
 
     def _geometry_of(self, M, N, K, dt):
-        from .ops_dot import _choose_instr
         if M % 16 or N % 16 or K % 16 or M < 16 or N < 16:
             return None
-        instr = _choose_instr(M, N, K, dt)
+        instr = self.pick_instr(M, N, K, dt)
         if lo.INSTR[instr][3] != 8:
             return None
         wm, wn, rep = self.wave_grid(M, N, instr)

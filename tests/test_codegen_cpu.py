@@ -123,11 +123,17 @@ def test_matmul_uses_mfma(dt, ptr):
     src, lds = compile_source(W.matmul_kernel, args,
                               {"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4,
                               num_stages=2)
-    assert f"newt::mfma_32x32x16" in src
+    assert "newt::mfma_32x32x16" in src
     assert 0 < lds <= 160 * 1024
     asm = isa(src)
     assert f"v_mfma_f32_32x32x16_{dt}" in asm
     assert "ds_read_b128" in asm
+    # 4 waves of 128x128 over one 32-deep k-step: the 16x16x32 MFMA
+    src, lds = compile_source(W.matmul_kernel, args,
+                              {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=4,
+                              num_stages=4)
+    assert "newt::mfma_16x16x32" in src and lds == 128 * 1024
+    assert f"v_mfma_f32_16x16x32_{dt}" in isa(src)
 
 
 def test_attention_compiles_with_mfma():
