@@ -45,6 +45,53 @@ def _has_row_reduction(fndef):
     return False
 
 
+def _split_dot_axes(fndef):
+    """True when some nl.dot's first operand depends on program axis 0 but not
+    axis 1 and its second on axis 1 but not axis 0 (or the reverse): the tiled
+    matmul pattern, in which program (i, j) reads row panel i of one operand
+    and column panel j of the other. Dependence is followed through
+    assignments by name (an over-approximation: it only ever adds axes, so an
+    unclear case is not matched)."""
+    taint = {}
+
+    def axes(expr):
+        out = set()
+        for n in ast.walk(expr):
+            if _callee_name(n) == "program_id":
+                arg = n.args[0] if n.args else next((k.value for k in n.keywords if k.arg == "axis"), None)
+                out.add(arg.value if isinstance(arg, ast.Constant) else -1)
+            elif isinstance(n, ast.Name) and n.id in taint:
+                out |= taint[n.id]
+        return out
+
+    changed = True
+    while changed:
+        changed = False
+        for n in ast.walk(fndef):
+            if isinstance(n, ast.Assign):
+                targets, value = n.targets, n.value
+            elif isinstance(n, (ast.AugAssign, ast.AnnAssign)) and n.value is not None:
+                targets, value = [n.target], n.value
+            elif isinstance(n, ast.For):
+                targets, value = [n.target], n.iter
+            else:
+                continue
+            t = axes(value)
+            for tg in targets:
+                for e in ast.walk(tg):
+                    if isinstance(e, ast.Name) and not t <= taint.get(e.id, set()):
+                        taint[e.id] = taint.get(e.id, set()) | t
+                        changed = True
+    for n in ast.walk(fndef):
+        if _callee_name(n) == "dot" and len(n.args) >= 2:
+            a, b = axes(n.args[0]), axes(n.args[1])
+            if -1 in a or -1 in b:
+                continue
+            if ({0, 1} & a, {0, 1} & b) in (({0}, {1}), ({1}, {0})):
+                return True
+    return False
+
+
 _MEM_WRITES = {"store", "atomic_add", "atomic_max", "atomic_min"}
 
 
@@ -127,6 +174,7 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
     fed to the next until no new hint appears."""
     hints = {}
     prefer_rows = _has_row_reduction(fndef)
+    group_pids = _split_dot_axes(fndef)
     # off by default: on memory-bound kernels the registers held by early loads
     # cost more occupancy than the overlap gains (layernorm 4096x8192: 86 -> 109
     # VGPRs, 5 -> 4 waves per SIMD, 7% slower)
@@ -137,6 +185,7 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
         cg = Compiler(fndef, fn_globals, params, constexprs, num_warps, kernel_name,
                       num_stages=num_stages, hints=hints, waves_per_eu=waves_per_eu)
         cg.prefer_rows = prefer_rows
+        cg.group_pids = group_pids
         try:
             src = cg.compile()
         except _Retry:

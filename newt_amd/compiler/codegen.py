@@ -155,6 +155,7 @@ class Codegen(ast.NodeVisitor):
         self.pipe_records = []
         self.pipe_active = None   # pipeline state while its loop body compiles
         self.pid_remap = False
+        self.group_pids = False   # set by compile_fn for matmul-shaped kernels
         self.params = params
         vec = 1
         for _, p in params:
@@ -1532,7 +1533,15 @@ class Codegen(ast.NodeVisitor):
         then share an L2, and a grid whose work varies along axis 0 (causal
         attention) is spread evenly over the XCDs instead of giving one XCD
         every eighth, heaviest block. Programs are independent, so any
-        bijection keeps the language's semantics (NEWT_PID_REMAP=0: identity)."""
+        bijection keeps the language's semantics (NEWT_PID_REMAP=0: identity).
+
+        In a kernel where program (i, j) reads row panel i of one dot operand
+        and column panel j of the other (group_pids), each XCD's range is
+        further walked in groups of G values of axis 0 with axis 1 varying
+        inside a group: the 32 or so programs an XCD runs at once then share
+        G row panels and about 32/G column panels instead of needing every
+        row panel, which keeps an 8192^3 fp16 matmul's operands in L2/MALL
+        (NEWT_PID_GROUP=G, default 4; 0 turns grouping off)."""
         ax = self._cx(node, axis, "program_id axis")
         if os.environ.get("NEWT_PID_REMAP", "1") == "0":
             return self.new_scalar(tp.int32, f"(int)blockIdx.{'xyz'[ax]}")
@@ -1544,10 +1553,22 @@ class Codegen(ast.NodeVisitor):
                 "unsigned _pb = blockIdx.x + _nbx * (blockIdx.y + _nby * blockIdx.z);",
                 "{ const unsigned _full = _nb & ~7u;",
                 "  if (_pb < _full) _pb = (_pb & 7u) * (_full >> 3) + (_pb >> 3); }",
-                "const int _pid0 = (int)(_pb % _nbx);",
-                "const int _pid1 = (int)((_pb / _nbx) % _nby);",
-                "const int _pid2 = (int)(_pb / (_nbx * _nby));",
             ]
+            G = int(os.environ.get("NEWT_PID_GROUP", "4")) if self.group_pids else 0
+            if G > 0:
+                self.prologue += [
+                    f"const unsigned _q = _pb % (_nbx * _nby), _gw = {G}u * _nby;",
+                    f"const unsigned _g0 = (_q / _gw) * {G}u;",
+                    f"const unsigned _gn = _nbx - _g0 < {G}u ? _nbx - _g0 : {G}u;",
+                    "const int _pid0 = (int)(_g0 + (_q % _gw) % _gn);",
+                    "const int _pid1 = (int)((_q % _gw) / _gn);",
+                ]
+            else:
+                self.prologue += [
+                    "const int _pid0 = (int)(_pb % _nbx);",
+                    "const int _pid1 = (int)((_pb / _nbx) % _nby);",
+                ]
+            self.prologue.append("const int _pid2 = (int)(_pb / (_nbx * _nby));")
         return Scalar(tp.int32, f"_pid{ax}", Sym(f"_pid{ax}", None, 1))
 
     def op_num_programs(self, node, axis):

@@ -305,3 +305,99 @@ def test_loads_do_not_move_across_stores():
     order = [ast.unparse(st).split(" =")[0].split("(")[0] for st in hoist_loads(fndef).body]
     # b may pass the reduction but not the store before it
     assert order == ["offs", "a", "nl.store", "b", "s", "nl.store"]
+
+
+def _matmul_args(ptr=F16P):
+    args = {"a_ptr": (ptr, A16), "b_ptr": (ptr, A16), "c_ptr": (ptr, A16)}
+    for n in ("M", "N", "K", "sam", "sbk", "scm"):
+        args[n] = (tp.int32, D16)
+    for n in ("sak", "sbn", "scn"):
+        args[n] = (tp.int32, {"eq1": True})
+    return args
+
+
+def test_split_dot_axes_detection():
+    """Grouped program ids are chosen for kernels whose dot operands follow
+    different program axes (a tiled matmul, either operand order), not where
+    an operand follows both (attention's q) or the ids are one axis."""
+    from newt_amd.compiler import _split_dot_axes
+
+    def mm_swapped(a_ptr, b_ptr, c_ptr, B: nl.constexpr):
+        r = nl.arange(0, B)
+        pn = nl.program_id(1)
+        pm = nl.program_id(axis=0)
+        x = nl.load(b_ptr + (pn * B + r)[:, None] * B + r[None, :])
+        y = nl.load(a_ptr + r[:, None] * B + (pm * B + r)[None, :])
+        nl.store(c_ptr + r[:, None] * B + r[None, :], nl.dot(x, y))
+
+    def one_axis(a_ptr, b_ptr, c_ptr, B: nl.constexpr, NPN: nl.constexpr):
+        pid = nl.program_id(0)
+        pm, pn = pid // NPN, pid % NPN
+        r = nl.arange(0, B)
+        x = nl.load(a_ptr + (pm * B + r)[:, None] * B + r[None, :])
+        y = nl.load(b_ptr + r[:, None] * B + (pn * B + r)[None, :])
+        nl.store(c_ptr + r[:, None] * B + r[None, :], nl.dot(x, y))
+
+    assert _split_dot_axes(fndef_of(W.matmul_kernel)[0])
+    assert _split_dot_axes(fndef_of(mm_swapped)[0])
+    assert not _split_dot_axes(fndef_of(one_axis)[0])
+    assert not _split_dot_axes(fndef_of(W.attention_kernel)[0])
+    assert not _split_dot_axes(fndef_of(W.softmax_kernel)[0])
+
+
+_PID_HARNESS = r"""
+#include <stdio.h>
+#include <stdlib.h>
+struct dim { unsigned x, y, z; };
+int main(int argc, char **argv) {
+  const struct dim gridDim = {atoi(argv[1]), atoi(argv[2]), atoi(argv[3])};
+  const unsigned n = gridDim.x * gridDim.y * gridDim.z;
+  unsigned *hits = calloc(n, sizeof(unsigned));
+  for (unsigned z = 0; z < gridDim.z; z++)
+    for (unsigned y = 0; y < gridDim.y; y++)
+      for (unsigned x = 0; x < gridDim.x; x++) {
+        const struct dim blockIdx = {x, y, z};
+%s
+        if (_pid0 < 0 || _pid1 < 0 || _pid2 < 0 || (unsigned)_pid0 >= gridDim.x ||
+            (unsigned)_pid1 >= gridDim.y || (unsigned)_pid2 >= gridDim.z) return 2;
+        hits[((unsigned)_pid2 * gridDim.y + (unsigned)_pid1) * gridDim.x + (unsigned)_pid0]++;
+      }
+  for (unsigned i = 0; i < n; i++) if (hits[i] != 1) return 3;
+  return 0;
+}
+"""
+
+
+@pytest.mark.parametrize("group", ["4", "8", "3", "0"])
+def test_program_id_mapping_is_a_bijection(monkeypatch, tmp_path, group):
+    """The program-id prologue the matmul kernel is compiled with, built with
+    gcc on the host and run over every workgroup id of ragged and even grids:
+    each program id is produced exactly once and in range (grouped for
+    NEWT_PID_GROUP=3/4/8, XCD remap only for 0)."""
+    monkeypatch.setenv("NEWT_PID_GROUP", group)
+    src, _ = compile_source(W.matmul_kernel, _matmul_args(),
+                            {"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 32}, num_warps=4)
+    lines = src.splitlines()
+    i0 = next(i for i, l in enumerate(lines) if "const unsigned _nbx" in l)
+    i1 = next(i for i, l in enumerate(lines) if "const int _pid2" in l)
+    prologue = "\n".join(lines[i0:i1 + 1])
+    assert ("_gw" in prologue) == (group != "0")
+    c = tmp_path / "pid.c"
+    c.write_text(_PID_HARNESS % prologue)
+    exe = tmp_path / "pid"
+    subprocess.run(["gcc", "-O1", "-o", str(exe), str(c)], check=True)
+    for g in ((32, 32, 1), (16, 16, 1), (13, 7, 2), (5, 4, 1), (1, 1, 1), (3, 100, 1),
+              (100, 3, 1), (9, 9, 3), (1, 17, 1), (17, 1, 1), (64, 48, 1)):
+        r = subprocess.run([str(exe)] + [str(v) for v in g])
+        assert r.returncode == 0, (g, r.returncode)
+
+
+def test_attention_program_ids_not_grouped():
+    args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
+    args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})
+    for n in ("sqb", "sqh", "sqm", "skb", "skh", "skn", "svb", "svh", "svn", "sob", "soh", "som"):
+        args[n] = (tp.int32, D16)
+    src, _ = compile_source(W.attention_kernel, args,
+                            {"BLOCK_M": 128, "BLOCK_N": 64, "D": 128, "CAUSAL": True},
+                            num_warps=4, num_stages=2)
+    assert "_pid0 = (int)(_pb % _nbx)" in src and "_gw" not in src
