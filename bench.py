@@ -338,10 +338,15 @@ def secondary():
                             "ms_flushed": round(ms, 5), "frac_hbm": round(v / PEAK_GBS, 4),
                             "ms_back_to_back": round(kern, 5), "bytes": work})
         from oracle import newt_oracle as orc
-        S = 4096
-        for dt, tuned, peak, name in (
-                (torch.bfloat16, W.matmul_tuned, PEAK_TFLOPS, "matmul bf16 4096^3"),
-                (torch.float32, W.matmul_tuned_fp32, PEAK_FP32_TFLOPS,
+        # the other square sizes and dtypes of the matmul configuration, each
+        # autotuned and checked like the headline; torch.mm (hipBLASLt) is timed
+        # beside the fp16/bf16 ones for context
+        for dt, S, tuned, peak, name in (
+                (torch.float16, 1024, W.matmul_tuned, PEAK_TFLOPS, "matmul fp16 1024^3"),
+                (torch.float16, 2048, W.matmul_tuned, PEAK_TFLOPS, "matmul fp16 2048^3"),
+                (torch.float16, 8192, W.matmul_tuned, PEAK_TFLOPS, "matmul fp16 8192^3"),
+                (torch.bfloat16, 4096, W.matmul_tuned, PEAK_TFLOPS, "matmul bf16 4096^3"),
+                (torch.float32, 4096, W.matmul_tuned_fp32, PEAK_FP32_TFLOPS,
                  "matmul fp32 4096^3 (fp32 MFMA, full precision; the reference runs tf32)")):
             a = seeded((S, S), 4, scale=S ** -0.5, dtype=dt)
             b = seeded((S, S), 5, scale=S ** -0.5, dtype=dt)
@@ -356,11 +361,19 @@ def secondary():
             cfg = tuned.best_config
             _, kern = timed_launches(lambda: W.matmul(a, b, c, config=cfg), 20)
             v = 2.0 * S ** 3 / (kern * 1e-3) / 1e12
-            res.append({"workload": name, "value": round(v, 2), "unit": "TFLOP/s",
-                        "ms": round(kern, 5), "frac_mfma": round(v / peak, 4),
-                        "rel_frobenius_vs_oracle": err,
-                        "tile": dict(cfg.kwargs), "num_warps": cfg.num_warps,
-                        "num_stages": cfg.num_stages})
+            line = {"workload": name, "value": round(v, 2), "unit": "TFLOP/s",
+                    "ms": round(kern, 5), "frac_mfma": round(v / peak, 4),
+                    "rel_frobenius_vs_oracle": err,
+                    "tile": dict(cfg.kwargs), "num_warps": cfg.num_warps,
+                    "num_stages": cfg.num_stages}
+            if dt != torch.float32:
+                for _ in range(3):
+                    torch.mm(a, b, out=c)
+                _, tk = timed_launches(lambda: torch.mm(a, b, out=c), 20)
+                line["torch_mm_tflops"] = round(2.0 * S ** 3 / (tk * 1e-3) / 1e12, 2)
+            res.append(line)
+            del a, b, c
+        S = 4096
         # deuteron: the same matmul written as tiles, traced to newt and
         # autotuned against its eager oracle (examples/deuteron/01_matmul.py)
         import tempfile
