@@ -234,10 +234,11 @@ __device__ __forceinline__ f32x4 mfma_16x16x4(float a, float b, f32x4 c) {
 // 256-byte bank line (SHIFT) and is chosen so that neither fragment pattern
 // (16x16x32: lane -> row l % 16, chunk l / 16; 32x32x16: row l % 32, chunk
 // l / 32) puts two lanes of one cycle on one slot:
-//   64-byte rows:  q ^ ((q & 1) << 1), q = (r >> 2) & 3 (conflict-free for both);
-//   128-byte rows: (r >> 1) & 7 (conflict-free for both);
-//   256-byte rows: r & 7 (2-way; a conflict-free key needs a third key bit in
-//   the chunk bits the k-step sets, i.e. an address per k-step).
+//   64-byte rows:  q ^ ((q & 1) << 1), q = (r >> 2) & 3;
+//   128-byte rows: (r >> 1) & 7;
+//   256-byte rows: r & 15 (every key of fewer bits leaves a conflict: the
+//   key's null space must avoid the lane offsets that share a cycle).
+// All three are conflict-free for both patterns.
 // ---------------------------------------------------------------------------
 template <typename T, int KD>
 struct LdsTile {
@@ -249,6 +250,7 @@ struct LdsTile {
   __host__ __device__ __forceinline__ static int key(int r) {
     const int q = (r >> SHIFT) & SWZ;
     if constexpr (CPR == 4) return q ^ ((q & 1) << 1);
+    else if constexpr (CPR == 16) return r & 15;
     else return q;
   }
   // element offset of (row r, reduction index k)

@@ -162,13 +162,9 @@ def test_r_major_tiles_are_bijective_and_conflict_free(layout_report):
         assert worst == 1, key
 
 
-def test_k_major_tiles(layout_report):
+def test_k_major_tiles_are_bijective_and_conflict_free(layout_report):
     k = {k: v for k, v in layout_report.items() if k[0] == "K"}
     assert len(k) == 6
     for key, (ok, worst) in k.items():
         assert ok == 1, key
-        # 256-byte rows (KD=128: attention's K tile, BLOCK_K=128 matmul A
-        # tiles) stay 2-way: no key confined to the lane-dependent chunk bits
-        # is conflict-free there, and a wider one costs an address register
-        # per k-step (measured as spills and a slower attention kernel).
-        assert worst == (2 if key[1] == 128 else 1), key
+        assert worst == 1, key
