@@ -122,6 +122,44 @@ class _Prepass:
                     out.add(n.id)
         return out
 
+    @staticmethod
+    def exposed(stmts):
+        """Names whose value on entry to `stmts` may be read: read before an
+        assignment that certainly runs first. Assignments inside loops and
+        branches are not certain to run; a loop body's own exposed reads are
+        exposed for the loop (except its target)."""
+        rd = _Prepass.read
+        live, defined = set(), set()
+        for st in stmts:
+            if isinstance(st, ast.Assign):
+                live |= rd([st.value] + st.targets) - defined
+                for t in st.targets:
+                    defined |= {e.id for e in ast.walk(t)
+                                if isinstance(e, ast.Name) and isinstance(e.ctx, ast.Store)}
+            elif isinstance(st, (ast.AugAssign, ast.AnnAssign)):
+                tgt = st.target.id if isinstance(st.target, ast.Name) else None
+                vals = [st.value] if st.value is not None else []
+                reads = rd(vals)
+                if isinstance(st, ast.AugAssign) and tgt is not None:
+                    reads |= {tgt}
+                live |= reads - defined
+                if tgt is not None:
+                    defined.add(tgt)
+            elif isinstance(st, ast.For):
+                inner = _Prepass.exposed(st.body)
+                if isinstance(st.target, ast.Name):
+                    inner = inner - {st.target.id}
+                live |= (rd([st.iter]) | inner | _Prepass.exposed(st.orelse)) - defined
+            elif isinstance(st, ast.While):
+                live |= (rd([st.test]) | _Prepass.exposed(st.body)
+                         | _Prepass.exposed(st.orelse)) - defined
+            elif isinstance(st, ast.If):
+                live |= (rd([st.test]) | _Prepass.exposed(st.body)
+                         | _Prepass.exposed(st.orelse)) - defined
+            else:
+                live |= rd([st]) - defined
+        return live
+
 
 class Codegen(ast.NodeVisitor):
     def __init__(self, fndef, fn_globals, params, constexprs, num_warps, kernel_name,
@@ -152,6 +190,7 @@ class Codegen(ast.NodeVisitor):
         self.body_stack = []
         self.dot_state = {}
         self.lds_arrays = []      # (name, bytes): distinct __shared__ arrays (pipeline stages)
+        self.lds_pool = []        # indices of lds_arrays freed by finished pipelined loops
         self.pipe_records = []
         self.pipe_active = None   # pipeline state while its loop body compiles
         self.pid_remap = False
@@ -773,16 +812,23 @@ class Codegen(ast.NodeVisitor):
                 self.body_stack.pop()
 
     def _read_after(self):
-        """Names read after the current statement in all enclosing bodies."""
+        """Names whose current values may be read after the current statement,
+        in any enclosing body (reads preceded by a reassignment that certainly
+        runs first do not count)."""
         out = set()
         for stmts, i in self.body_stack:
-            out |= _Prepass.read(stmts[i + 1:])
+            out |= _Prepass.exposed(stmts[i + 1:])
         return out
 
     def _enter_compound(self, node):
         """Create storage for names that the statement reassigns (loop-carried)
-        and register placeholders for names it defines and that are read later."""
+        and register placeholders for names it defines and that are read later.
+        A for loop's target is not loop-carried: the loop header rebinds it on
+        every trip (an earlier binding of the name, e.g. the target of a
+        previous loop, is not its initial value)."""
         assigned = _Prepass.assigned(node)
+        if isinstance(node, ast.For) and isinstance(node.target, ast.Name):
+            assigned = assigned - {node.target.id}
         for name in sorted(assigned):
             if name in self.locals:
                 v = self.locals[name]
@@ -796,7 +842,8 @@ class Codegen(ast.NodeVisitor):
         hoist = {n for n in assigned if n not in self.locals and n in after}
         if isinstance(node, ast.For) and isinstance(node.target, ast.Name):
             hoist.discard(node.target.id)
-        rec = {"names": hoist, "index": len(self.lines), "indent": self.indent, "node": node}
+        rec = {"names": hoist, "index": len(self.lines), "indent": self.indent, "node": node,
+               "pre": set(self.locals) | set(self.storages)}
         self.pending_hoist.append(rec)
         return rec
 
@@ -804,7 +851,13 @@ class Codegen(ast.NodeVisitor):
         return False
 
     def _exit_compound(self, rec):
+        """Names first defined inside the statement and not read after it are
+        scoped to its C block: drop their bindings, so a later statement that
+        assigns the same name starts fresh instead of carrying a stale value."""
         self.pending_hoist.remove(rec)
+        for name in _Prepass.assigned(rec["node"]) - rec["pre"] - rec["names"]:
+            if name not in self.storages:
+                self.locals.pop(name, None)
 
     def visit_For(self, node):
         self.flush_loads()
@@ -854,7 +907,13 @@ class Codegen(ast.NodeVisitor):
         self.indent -= 1
         self.emit("}")
         self._exit_compound(rec)
+        self.end_loop_target(node)
         self.after_loop(node)
+
+    def end_loop_target(self, node):
+        """The loop counter is scoped to the C loop; after the loop the target
+        name is unbound (reading it is an undefined-name error)."""
+        self.locals.pop(node.target.id, None)
 
     def visit_While(self, node):
         self.flush_loads()

@@ -349,7 +349,10 @@ class DotPipeline:
         if state["plr"]:
             self._insert_lines(mark, self._plr_preamble(state, n))
         self._exit_compound(rec)
+        self.end_loop_target(node)
         self.after_loop(node)
+        if state["recs"] is not None:
+            self.lds_pool.extend(state["lds_idx"])
 
     def _insert_lines(self, index, lines):
         ind = "  " * self.indent
@@ -574,12 +577,27 @@ class DotPipeline:
                 V.consumed = True
                 if V in self.pending_loads:
                     self.pending_loads.remove(V)
-        names = []
+        # stage arrays of a pipelined loop that has finished are reused (a
+        # later loop never needs them at the same time); a barrier first lets
+        # every wave finish reading them before this loop's copies land. A loop
+        # nested in another rewrites its stages on each outer trip: same barrier
+        names, idx = [], []
+        reused = False
         for _ in range(state["S"]):
-            nm = f"_ldsP{len(self.lds_arrays)}"
-            self.lds_arrays.append((nm, off))
+            if self.lds_pool:
+                i = self.lds_pool.pop(0)
+                nm, sz = self.lds_arrays[i]
+                self.lds_arrays[i] = (nm, max(sz, off))
+                reused = True
+            else:
+                i = len(self.lds_arrays)
+                nm = f"_ldsP{i}"
+                self.lds_arrays.append((nm, off))
             names.append(nm)
-        state.update(recs=recs, ops=ops, names=names)
+            idx.append(i)
+        if reused or self.loop_depth > 0:
+            self.emit("__syncthreads();")
+        state.update(recs=recs, ops=ops, names=names, lds_idx=idx)
 
     def pipe_issue(self, state, slot, valid, fast=False):
         if state["recs"] is None:

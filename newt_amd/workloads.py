@@ -215,22 +215,41 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
     l_i = nl.zeros((BLOCK_M,), dtype=nl.float32)
     acc = nl.zeros((BLOCK_M, D), dtype=nl.float32)
 
+    # key blocks wholly inside the sequence (and, causal, wholly below the
+    # diagonal of every row of this program) need no mask; the ragged tail and
+    # the diagonal blocks run in a second, masked loop. Scores stay unscaled:
+    # the scale is applied inside the exponent's fma, and the running max is
+    # max(qk) * qk_scale (= max(qk * qk_scale): rounding is monotonic).
+    full_n = S // BLOCK_N * BLOCK_N
     end_n = S
     if CAUSAL:
+        full_n = nl.minimum(full_n, pid * BLOCK_M // BLOCK_N * BLOCK_N)
         end_n = nl.minimum(S, (pid + 1) * BLOCK_M)
-    for start_n in range(0, end_n, BLOCK_N):
+    for start_n in range(0, full_n, BLOCK_N):
+        offs_n = start_n + nl.arange(0, BLOCK_N)
+        k = nl.load(k_base + offs_n[:, None] * skn + offs_d[None, :])
+        qk = nl.dot(q, nl.trans(k))
+        m_new = nl.maximum(m_i, nl.max(qk, axis=1) * qk_scale)
+        alpha = nl.exp2(m_i - m_new)
+        p = nl.exp2(nl.fma(qk, qk_scale, -m_new[:, None]))
+        l_i = l_i * alpha + nl.sum(p, axis=1)
+        acc = acc * alpha[:, None]
+        v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :])
+        acc = nl.dot(p.to(v_ptr.dtype.element_ty), v, acc)
+        m_i = m_new
+    for start_n in range(full_n, end_n, BLOCK_N):
         offs_n = start_n + nl.arange(0, BLOCK_N)
         nmask = offs_n[:, None] < S
         k = nl.load(k_base + offs_n[:, None] * skn + offs_d[None, :], mask=nmask, other=0.0)
-        qk = nl.dot(q, nl.trans(k)) * qk_scale
+        qk = nl.dot(q, nl.trans(k))
         if CAUSAL:
             qk = nl.where((offs_m[:, None] >= offs_n[None, :]) & (offs_n[None, :] < S),
                           qk, float("-inf"))
         else:
             qk = nl.where(offs_n[None, :] < S, qk, float("-inf"))
-        m_new = nl.maximum(m_i, nl.max(qk, axis=1))
+        m_new = nl.maximum(m_i, nl.max(qk, axis=1) * qk_scale)
         alpha = nl.exp2(m_i - m_new)
-        p = nl.exp2(qk - m_new[:, None])
+        p = nl.exp2(nl.fma(qk, qk_scale, -m_new[:, None]))
         l_i = l_i * alpha + nl.sum(p, axis=1)
         acc = acc * alpha[:, None]
         v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :], mask=nmask, other=0.0)

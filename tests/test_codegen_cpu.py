@@ -401,3 +401,46 @@ def test_attention_program_ids_not_grouped():
                             {"BLOCK_M": 128, "BLOCK_N": 64, "D": 128, "CAUSAL": True},
                             num_warps=4, num_stages=2)
     assert "_pid0 = (int)(_pb % _nbx)" in src and "_gw" not in src
+
+
+def test_loops_reusing_a_target_name_compile():
+    """Two loops with the same target name: the second loop's target is not
+    loop-carried state initialised from the first loop's (out-of-scope)
+    counter, and the name is unbound after each loop."""
+    def k(x_ptr, o_ptr, n, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        acc = nl.zeros((BLOCK,), dtype=nl.float32)
+        for i in range(0, n, 2):
+            acc = acc + nl.load(x_ptr + i * BLOCK + offs)
+        for i in range(1, n, 2):
+            acc = acc - nl.load(x_ptr + i * BLOCK + offs)
+        nl.store(o_ptr + offs, acc)
+
+    src, _ = compile_source(k, {"x_ptr": F32P, "o_ptr": F32P, "n": tp.int32}, {"BLOCK": 64})
+    isa(src)   # compiles with hipRTC
+
+    def reads_target_after_loop(o_ptr, n, BLOCK: nl.constexpr):
+        for i in range(n):
+            pass
+        nl.store(o_ptr + nl.arange(0, BLOCK), nl.zeros((BLOCK,), dtype=nl.float32) + i)
+
+    with pytest.raises(CompileError):
+        compile_source(reads_target_after_loop, {"o_ptr": F32P, "n": tp.int32}, {"BLOCK": 64})
+
+
+def test_sequential_pipelined_loops_share_lds_stages():
+    """Attention's unmasked key loop and its masked tail loop are both
+    pipelined (direct-to-LDS copies, branch-free fast copy), and the second
+    reuses the first one's stage arrays after a barrier: the kernel needs the
+    LDS of one loop (2 stages x (K + V) = 64 KiB), not of two."""
+    args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
+    args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})
+    for n in ("sqb", "sqh", "sqm", "skb", "skh", "skn", "svb", "svh", "svn", "sob", "soh", "som"):
+        args[n] = (tp.int32, D16)
+    for causal in (False, True):
+        src, lds = compile_source(W.attention_kernel, args,
+                                  {"BLOCK_M": 128, "BLOCK_N": 64, "D": 128, "CAUSAL": causal},
+                                  num_warps=4, num_stages=2, waves_per_eu=2)
+        assert lds == 64 * 1024
+        assert len(re.findall(r"for \(; _it\d+ \+ 2 <", src)) == 2   # two fast copies
+        assert src.count("newt::lds_dma16(") >= 16

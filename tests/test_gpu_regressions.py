@@ -2,6 +2,7 @@
 that need a launch, with the same known answers:
   values defined inside a loop / both branches of an if, read after it    :12-40
   `prev = x` inside a loop is a copy, not an alias                        :43-58
+  two loops reusing one target name (here: the second is not loop-carried)
   bool max / sum give "any" and a count (1 and 3; 0 and 0)               :85-100
   an atomic through a scalar pointer fires once per program (10.0)        :103-111
   float atomic_max over 4 programs == x.max()                             :114-124
@@ -56,6 +57,23 @@ def test_value_defined_in_both_branches():
     assert torch.equal(y, x * 2)
     k[(1,)](x, y, 0, BLOCK=64)
     assert torch.equal(y, x * 3)
+
+
+def test_two_loops_share_a_target_name():
+    @newt.jit
+    def k(x_ptr, o_ptr, n, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        acc = nl.zeros((BLOCK,), dtype=nl.float32)
+        for i in range(0, n, 2):
+            acc = acc + nl.load(x_ptr + i * BLOCK + offs)
+        for i in range(1, n, 2):
+            acc = acc - nl.load(x_ptr + i * BLOCK + offs)
+        nl.store(o_ptr + offs, acc)
+
+    x = torch.randn(7, 64, device="cuda")
+    o = torch.empty(64, device="cuda")
+    k[(1,)](x, o, 7, BLOCK=64)
+    torch.testing.assert_close(o, x[0::2].sum(0) - x[1::2].sum(0), rtol=1e-5, atol=1e-5)
 
 
 def test_copy_in_loop_does_not_alias():
