@@ -99,6 +99,16 @@ int newt_launch_packed(newt_function_t function, unsigned gx, unsigned gy,
                        unsigned gz, unsigned block, unsigned lds_bytes,
                        void* stream, const void* argbuf, size_t argsize);
 
+/* newt_launch_packed, with two HIP events (hipEvent_t, either may be NULL)
+ * that the dispatch itself records when the kernel starts and ends
+ * (hipExtModuleLaunchKernel): per-launch kernel times without separate
+ * event-record packets between back-to-back launches. No reference
+ * counterpart; bench.py times its launches with it. */
+int newt_launch_packed_timed(newt_function_t function, unsigned gx, unsigned gy,
+                             unsigned gz, unsigned block, unsigned lds_bytes,
+                             void* stream, const void* argbuf, size_t argsize,
+                             void* ev_start, void* ev_stop);
+
 /* gcnArchName of a device (e.g. "gfx950:sramecc+:xnack-") into buf.
  * Replaces: _arch() / torch.cuda.get_device_capability (newt/runtime/jit.py:26-32). */
 int newt_device_arch(int device, char* buf, size_t buflen);

@@ -302,6 +302,40 @@ int newt_launch_packed(newt_function_t function, unsigned gx, unsigned gy, unsig
   return NEWT_OK;
 }
 
+// libamdhip64's launch with events recorded by the dispatch packet (declared
+// here: hip_ext.h also holds templates that need the HIP compiler, and this
+// file is plain C++)
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent,
+                                               hipEvent_t stopEvent, uint32_t flags);
+
+int newt_launch_packed_timed(newt_function_t function, unsigned gx, unsigned gy, unsigned gz,
+                             unsigned block, unsigned lds_bytes, void* stream,
+                             const void* argbuf, size_t argsize, void* ev_start,
+                             void* ev_stop) {
+  if (!function) return fail(NEWT_ERR_INVALID, "newt_launch_packed_timed: null function");
+  if (block == 0 || block > 1024 || gx == 0 || gy == 0 || gz == 0)
+    return fail(NEWT_ERR_INVALID, "newt_launch_packed_timed: bad launch shape");
+  // this launch API takes work-item counts, not workgroup counts
+  if ((unsigned long long)gx * block > 0xffffffffull)
+    return fail(NEWT_ERR_INVALID, "newt_launch_packed_timed: grid too large");
+  size_t size = argsize;
+  static const unsigned long long empty = 0;
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER,
+                    const_cast<void*>(argsize ? argbuf : &empty),
+                    HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+  hipError_t e = hipExtModuleLaunchKernel(function->fn, gx * block, gy, gz, block, 1, 1,
+                                          lds_bytes, static_cast<hipStream_t>(stream),
+                                          nullptr, config, static_cast<hipEvent_t>(ev_start),
+                                          static_cast<hipEvent_t>(ev_stop), 0);
+  if (e != hipSuccess) return hip_fail(e, "hipExtModuleLaunchKernel");
+  return NEWT_OK;
+}
+
 int newt_device_arch(int device, char* buf, size_t buflen) {
   if (!buf || buflen == 0) return fail(NEWT_ERR_INVALID, "newt_device_arch: null buffer");
   hipDeviceProp_t prop;

@@ -70,6 +70,8 @@ def lib():
                               ctypes.POINTER(c_void_p)]
     L.newt_launch_packed.argtypes = [c_void_p, c_uint, c_uint, c_uint, c_uint, c_uint,
                                      c_void_p, c_char_p, c_size_t]
+    L.newt_launch_packed_timed.argtypes = [c_void_p, c_uint, c_uint, c_uint, c_uint, c_uint,
+                                           c_void_p, c_char_p, c_size_t, c_void_p, c_void_p]
     L.newt_device_arch.argtypes = [c_int, c_char_p, c_size_t]
     L.newt_device_limits.argtypes = [c_int] + [ctypes.POINTER(c_int)] * 3
     if L.newt_abi_version() != 1:
@@ -173,6 +175,14 @@ class Kernel:
                                           stream, argbuf, len(argbuf))
         if st != 0:
             _check(st, "hipModuleLaunchKernel")
+
+    def launch_packed_timed(self, gx, gy, gz, block, stream, argbuf, ev_start, ev_stop):
+        """launch_packed with two hipEvent_t handles recorded by the dispatch
+        itself at the kernel's start and end."""
+        st = self._lib.newt_launch_packed_timed(self.func, gx, gy, gz, block, self.lds_bytes,
+                                                stream, argbuf, len(argbuf), ev_start, ev_stop)
+        if st != 0:
+            _check(st, "hipExtModuleLaunchKernel")
 
 
 # struct codes and alignment of each kernel parameter kind in the packed

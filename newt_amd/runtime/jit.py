@@ -32,6 +32,11 @@ from . import hip as _hip
 
 
 # environment switches that change generated code (part of the specialization key)
+# Timing hook: None, or a callable returning the (start, stop) hipEvent_t
+# handles that the next launch's dispatch records at the kernel's start and end
+# (a benchmark sets it around its timed launches).
+launch_events = None
+
 _CODEGEN_ENV = ("NEWT_VEC", "NEWT_PIPELINE_DOT", "NEWT_LDS_DMA", "NEWT_MFMA", "NEWT_PID_REMAP",
                 "NEWT_PIPE_VERSION", "NEWT_PLR", "NEWT_SCHED", "NEWT_HOIST_LOADS", "NEWT_PID_GROUP")
 _CODEGEN_ENV_B = tuple(k.encode() for k in _CODEGEN_ENV)
@@ -130,8 +135,13 @@ class CompiledKernel:
 
     def launch(self, grid, values, stream):
         gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
-        self.kernel.launch_packed(gx, gy, gz, 64 * self.num_warps, stream,
-                                  self.packer.pack(*values))
+        ev = launch_events
+        if ev is None:
+            self.kernel.launch_packed(gx, gy, gz, 64 * self.num_warps, stream,
+                                      self.packer.pack(*values))
+        else:
+            self.kernel.launch_packed_timed(gx, gy, gz, 64 * self.num_warps, stream,
+                                            self.packer.pack(*values), *ev())
 
 
 class JITFunction:
