@@ -41,6 +41,49 @@ def test_saxpy_both_launch_paths():
     assert torch.allclose(out, ref, atol=1e-5)
 
 
+def test_timed_launch_records_events_and_computes():
+    """newt_launch_packed_timed: same results as launch_packed, the two events
+    are recorded by the dispatch (elapsed time positive), a NULL pair is
+    accepted, and a ragged 2D grid (work-item counts = grid x block) covers
+    every element exactly once."""
+    from newt_amd.runtime.hip import Kernel, compile_hip, pack_format
+
+    src = SRC + r"""
+extern "C" __global__ void mark(int* out, int nx, int ny) {
+    int x = blockIdx.x * blockDim.x + threadIdx.x, y = blockIdx.y;
+    if (x < nx && y < ny) atomicAdd(out + y * nx + x, 1);
+}
+"""
+    code = compile_hip(src, "saxpy")
+    k = Kernel(code, "saxpy")
+    n = (1 << 20) + 77
+    x = torch.randn(n, device="cuda")
+    y = torch.randn(n, device="cuda")
+    out = torch.empty_like(x)
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = ctypes.CDLL("libamdhip64.so")
+    evs = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for e in evs:
+        assert lib.hipEventCreate(ctypes.byref(e)) == 0
+    buf = pack_format(["f32", "ptr", "ptr", "ptr", "i32"]).pack(
+        2.5, x.data_ptr(), y.data_ptr(), out.data_ptr(), n)
+    k.launch_packed_timed((n + 255) // 256, 1, 1, 256, stream, buf, evs[0].value, evs[1].value)
+    torch.cuda.synchronize()
+    assert torch.allclose(out, (2.5 * x.double() + y.double()).float(), atol=1e-5)
+    ms = ctypes.c_float()
+    assert lib.hipEventElapsedTime(ctypes.byref(ms), evs[0], evs[1]) == 0
+    assert 0.0 < ms.value < 100.0
+    for e in evs:
+        lib.hipEventDestroy(e)
+    m = Kernel(code, "mark")
+    nx, ny = 1000, 3
+    hits = torch.zeros(ny * nx, device="cuda", dtype=torch.int32)
+    buf = pack_format(["ptr", "i32", "i32"]).pack(hits.data_ptr(), nx, ny)
+    m.launch_packed_timed((nx + 127) // 128, ny, 1, 128, stream, buf, None, None)
+    torch.cuda.synchronize()
+    assert bool((hits == 1).all())
+
+
 def test_device_is_gfx950():
     from newt_amd.runtime.hip import device_arch, device_limits
     assert device_arch(0).startswith("gfx950")
