@@ -198,6 +198,10 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
                      BLOCK_M: nl.constexpr, BLOCK_N: nl.constexpr, D: nl.constexpr,
                      CAUSAL: nl.constexpr):
     pid = nl.program_id(0)
+    if CAUSAL:
+        # query block i does i + 1 key blocks: launch the heaviest first so the
+        # last programs to start are short ones (a shorter tail)
+        pid = nl.num_programs(0) - 1 - pid
     bh = nl.program_id(1)
     bi = bh // H
     hi = bh % H
