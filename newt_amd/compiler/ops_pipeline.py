@@ -320,6 +320,10 @@ class DotPipeline:
         plr_env = os.environ.get("NEWT_PLR", "auto")
         state["plr"] = S >= 3 and (plr_env == "1" or (plr_env == "auto" and simple))
         state["simple"] = simple
+        # a loop body with a dot and an exponential (flash attention) takes
+        # LLVM's exp/MFMA interleave strategy in its branch-free copy
+        state["exp_mix"] = ndots > 0 and any(_callee(nd) in ("exp", "exp2")
+                                             for x in compute for nd in ast.walk(x))
         state["pf"] = {}
         self.pipe_records.append(state)
         for s in range(S - 1):
@@ -482,6 +486,8 @@ class DotPipeline:
                 self.emit("newt::wait_vmcnt<0>();")
             self.emit("__syncthreads();")
             self.emit("__builtin_amdgcn_sched_barrier(0);")
+            if fast and state["exp_mix"] and os.environ.get("NEWT_IGLP", "1") != "0":
+                self.emit("__builtin_amdgcn_iglp_opt(2);")
             # issue iteration it+S-1 into the stage that iteration it-1 read
             self.locals[kname] = self.new_scalar(idt, f"({lo_e} + ({it} + {S - 1}) * {stv})")
             self.visit_body(slice_stmts)
