@@ -563,14 +563,20 @@ class DotPipeline:
             if not isinstance(X, LazyLoad) or X.result is not None or len(X.shape) != 2:
                 self._no_pipe(state)
             dt = X.dtype
-            if dt not in (tp.float16, tp.bfloat16):
+            if dt not in (tp.float16, tp.bfloat16, tp.float32):
                 self._no_pipe(state)
             kdim = info["kdim"]
             V = X if kdim == 1 else self.permute(X, (1, 0))   # [R, K] view
             R, K = V.shape
-            if K % 16 or R % 16:
+            if K % (8 if dt == tp.float32 else 16) or R % 16:
                 self._no_pipe(state)
             fmt = self._tile_format(X, kdim)
+            if dt == tp.float32:
+                # fp32 fragments are read four k at a time (fragment prefetch
+                # holds 16-bit fragments only); R-major fp32 tiles need >= 64 rows
+                state["plr"] = False
+                if fmt == "r" and R % 64:
+                    self._no_pipe(state)
             nbytes = self.tile_bytes(R, K, dt)
             dma = self._dma_ok(V, fmt, R, K, dt) and os.environ.get("NEWT_LDS_DMA", "1") != "0"
             epc = 16 // dt.itemsize
@@ -667,6 +673,8 @@ class DotPipeline:
             self.emit("int _r, _k;")
             if fmt == "k":
                 self.emit(f"newt::lds_tile_slot<{T}, {K}>(_s, _r, _k);")
+            elif dt == tp.float32:
+                self.emit(f"newt::LdsTileR32<{R}>::slot(_s, _k, _r);")
             else:
                 self.emit(f"newt::LdsTileR<{T}, {R}>::slot(_s, _k, _r);")
             terms = [] if (off.base.is_const and off.base.const == 0) else [off.base.expr]
@@ -712,6 +720,7 @@ class DotPipeline:
             rr = self.coord(L, 0, s)
             kk = self.coord(L, 1, s)
             o = (f"newt::LdsTile<{T}, {K}>::off({rr}, {kk})" if fmt == "k"
+                 else f"newt::LdsTileR32<{R}>::off({kk}, {rr})" if dt == tp.float32
                  else f"newt::LdsTileR<{T}, {R}>::off({kk}, {rr})")
             if chunk > 1:
                 self.emit(f"newt::store_vec<{T}, {chunk}>({tile} + {o}, {r.var} + {s});")
@@ -720,6 +729,61 @@ class DotPipeline:
         if canon:
             self.indent -= 1
             self.emit("}")
+
+    def _staged_dot_f32(self, node, a, b, acc, M, N, K, instr, wm, wn, rep, state):
+        """fp32 nl.dot from pipeline stages on the 32x32x2 MFMA. Within each
+        group of 8 k, MFMA t contracts k = kk + t (lanes 0-31) and kk + 4 + t
+        (lanes 32-63): a lane's four k of one row are contiguous, one 16-byte
+        read of a K-major tile (four 4-byte reads of an R-major one) feeds four
+        MFMAs, and both operands use the same order."""
+        if rep > 1 or instr != "32x32x2" or K % 8:
+            self._no_pipe(state)
+        Bt = Staged(b.rec, b.slot, not b.trans) if isinstance(b, Staged) else None
+        if not isinstance(a, Staged) or Bt is None:
+            self._no_pipe(state)
+        Lc = self.mfma_layout(M, N, instr, wm, wn, 1)
+        RM, RN = M // wm // 32, N // wn // 32
+        orient = self.dot_orient()
+        accv = self.init_acc(node, acc, Lc, M, N)
+        self.emit("{")
+        self.indent += 1
+        self.emit(f"const int _ra = (_wave & {wm - 1}) * {M // wm};")
+        self.emit(f"const int _rb = ((_wave >> {lo.log2i(wm)}) & {wn - 1}) * {N // wn};")
+        self.emit("const int _kh = 4 * (_lane >> 5);")
+        tiles = []
+        for idx, X in enumerate((a, Bt)):
+            nm = f"_pt{idx}"
+            self.emit(f"const float* {nm} = (const float*)({state['names'][X.slot]} + "
+                      f"{X.rec['off']});")
+            tiles.append(nm)
+
+        def group(idx, X, r0, kk):
+            # the record describes the tile's [R, K] view (R = M for A, N for B)
+            rec, tile = X.rec, tiles[idx]
+            if rec["fmt"] == "k":
+                return f"newt::lds_frag_k32f<{rec['K']}>({tile}, {r0}, {kk}, _lane)"
+            c = f"({r0} + (_lane & 31))"
+            els = ", ".join(f"{tile}[newt::LdsTileR32<{rec['R']}>::off({kk} + _kh + {t}, {c})]"
+                            for t in range(4))
+            return f"f32x4{{{els}}}"
+
+        for g in range(K // 8):
+            kk = 8 * g
+            for i in range(RM):
+                self.emit(f"const f32x4 _fa{g}_{i} = {group(0, a, f'_ra + {i * 32}', kk)};")
+            for j in range(RN):
+                self.emit(f"const f32x4 _fb{g}_{j} = {group(1, Bt, f'_rb + {j * 32}', kk)};")
+            for t in range(4):
+                for i in range(RM):
+                    for j in range(RN):
+                        fa_, fb_ = f"_fa{g}_{i}[{t}]", f"_fb{g}_{j}[{t}]"
+                        x, y = (fb_, fa_) if orient == "row" else (fa_, fb_)
+                        v = f"{accv.var}[{j + RN * i}]"
+                        self.emit(f"{v} = newt::mfma_{instr}({x}, {y}, {v});")
+        state["sched"] = None
+        self.indent -= 1
+        self.emit("}")
+        return accv
 
     # ------------------------------------------------- loop-invariant operands
     def _dot_operand_shape(self, a, state):
@@ -798,6 +862,8 @@ class DotPipeline:
         M, N, K, dt, instr, wm, wn, rep = self.dot_geometry(node, a, b)
         MI, NI, KI, kpl, nacc = lo.INSTR[instr]
         state = getattr(self, "pipe_active", None)
+        if dt == tp.float32 and state is not None:
+            return self._staged_dot_f32(node, a, b, acc, M, N, K, instr, wm, wn, rep, state)
         if rep > 1 or kpl != 8 or dt not in (tp.float16, tp.bfloat16) or state is None:
             if state is not None:
                 self._no_pipe(state)

@@ -310,6 +310,24 @@ struct LdsTileR {
   }
 };
 
+// fp32 operand tiles stored with the row index contiguous: a [KD][RD] array of
+// floats (RD >= 64). Fragments of the fp32 MFMA are read one float per lane
+// (ds_read_b32), lanes 0-31 from k-row kk+t and lanes 32-63 from k-row
+// kk+4+t of the same 32 rows; the 128-byte halves of a k-row are swapped by
+// bit 2 of k so those two k-rows fall in different halves of the 64 banks.
+template <int RD>
+struct LdsTileR32 {
+  static_assert(RD >= 64 && RD % 64 == 0, "fp32 R-major tiles hold >= 64 rows");
+  __host__ __device__ __forceinline__ static int off(int k, int r) {
+    return k * RD + (r ^ (((k >> 2) & 1) << 5));
+  }
+  // (k, first r) of the 4-float chunk at physical chunk index `slot`
+  __host__ __device__ __forceinline__ static void slot(int s, int& k, int& r) {
+    k = s / (RD / 4);
+    r = ((s % (RD / 4)) * 4) ^ (((k >> 2) & 1) << 5);
+  }
+};
+
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // One MFMA operand fragment (8 consecutive k of one operand row per lane) from
@@ -368,11 +386,27 @@ __host__ __device__ __forceinline__ void frag_k_coords(int r0, int kk, int lane,
   k = kk + 8 * (lane / MI);
 }
 
+__host__ __device__ __forceinline__ void frag_k32f_coords(int r0, int kk, int lane, int& r,
+                                                          int& k) {
+  r = r0 + (lane & 31);
+  k = kk + 4 * (lane >> 5);
+}
+
 template <typename T, int KD, int MI>
 __device__ __forceinline__ i16x8 lds_frag_k(const T* tile, int r0, int kk, int lane) {
   int r, k;
   frag_k_coords<MI>(r0, kk, lane, r, k);
   return *(const i16x8*)(tile + LdsTile<T, KD>::off(r, k));
+}
+
+// fp32 fragment group of a K-major tile for the 32x32x2 MFMA in the permuted
+// k order: lane l gets row r0 + (l % 32) and k = kk + 4 * (l / 32) + 0..3, one
+// float for each of four MFMAs (MFMA t contracts k = kk + t and kk + 4 + t).
+template <int KD>
+__device__ __forceinline__ f32x4 lds_frag_k32f(const float* tile, int r0, int kk, int lane) {
+  int r, k;
+  frag_k32f_coords(r0, kk, lane, r, k);
+  return *(const f32x4*)(tile + LdsTile<float, KD>::off(r, k));
 }
 
 // Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4):

@@ -162,12 +162,13 @@ MATMUL_CONFIGS = [
 matmul_tuned = newt.autotune(configs=MATMUL_CONFIGS, key=["M", "N", "K"])(matmul_kernel)
 
 # fp32 operands run on the fp32 MFMA (v_mfma_f32_32x32x2_f32, full precision;
-# gfx950 has no tf32) with synchronous LDS staging: smaller k-steps, one stage
+# gfx950 has no tf32) through the same pipelined k-loop: 16-deep k-steps keep
+# 3-4 fp32 stages within the LDS
 MATMUL_CONFIGS_FP32 = [
-    newt.Config({"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 16}, num_warps=8, num_stages=1),
-    newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 16}, num_warps=8, num_stages=1),
-    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 16}, num_warps=4, num_stages=1),
-    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=4, num_stages=1),
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 16}, num_warps=8, num_stages=3),
+    newt.Config({"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 16}, num_warps=8, num_stages=4),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=4, num_stages=3),
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 16}, num_warps=4, num_stages=4),
 ]
 matmul_tuned_fp32 = newt.autotune(configs=MATMUL_CONFIGS_FP32, key=["M", "N", "K"])(matmul_kernel)
 

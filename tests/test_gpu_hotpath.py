@@ -150,6 +150,40 @@ def test_matmul_transposed_operands(W, dtype, M, N, K, ta, tb):
     assert orc.rel_frobenius(npf(c), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("cfg", [(256, 256, 16, 8, 3), (256, 128, 16, 8, 4), (128, 128, 32, 4, 3),
+                                 (128, 128, 16, 4, 4)])
+@pytest.mark.parametrize("M,N,K", [(512, 384, 256), (300, 200, 136), (1024, 1024, 512)])
+def test_matmul_fp32_pipelined(W, M, N, K, cfg):
+    """fp32 operands through the pipelined k-loop (direct-to-LDS stages, four
+    k per fragment read in the permuted order, ragged tails): full precision,
+    relative Frobenius error <= 1e-5 against the float64 oracle."""
+    import newt_amd as newt
+    a = seeded((M, K), 34, scale=K ** -0.5)
+    b = seeded((K, N), 35, scale=K ** -0.5)
+    BM, BN, BK, nw, ns = cfg
+    print(f"matmul_fp32_pipelined M={M} N={N} K={K} cfg={cfg}", flush=True)
+    c = W.matmul(a, b, config=newt.Config({"BLOCK_M": BM, "BLOCK_N": BN, "BLOCK_K": BK},
+                                         num_warps=nw, num_stages=ns))
+    ref = orc.matmul(npf(a), npf(b), "float32")
+    assert orc.rel_frobenius(npf(c), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("ta,tb", [(False, True), (True, False), (True, True)])
+def test_matmul_fp32_transposed_operands(W, ta, tb):
+    """Column-major fp32 A (an R-major tile read four floats at a time) and
+    K-contiguous B (a K-major tile read with 16-byte loads)."""
+    import newt_amd as newt
+    M, N, K = 384, 256, 200
+    a = seeded((K, M) if ta else (M, K), 36, scale=K ** -0.5)
+    b = seeded((N, K) if tb else (K, N), 37, scale=K ** -0.5)
+    a = a.t() if ta else a
+    b = b.t() if tb else b
+    c = W.matmul(a, b, config=newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 16},
+                                         num_warps=4, num_stages=3))
+    ref = orc.matmul(npf(a), npf(b), "float32")
+    assert orc.rel_frobenius(npf(c), ref) <= 1e-5
+
+
 @pytest.mark.parametrize("cfg", [(256, 256, 32, 4, 4), (256, 256, 32, 8, 4), (128, 128, 64, 4, 3)])
 def test_matmul_strided_rows(W, cfg):
     """Row strides larger than the row (views into a wider buffer) and an
