@@ -88,6 +88,36 @@ void check_r() {
   printf("R %d %d %d %d %d %d\n", RD, KD, MI, (int)PERM, (int)ok, worst);
 }
 
+// fp32 R-major [KD][RD] tile read four floats per lane in the permuted k order
+// of the 32x32x2 MFMA (lanes 0-31: k-row kk+t, lanes 32-63: kk+4+t), 4-byte
+// reads served 64 lanes per cycle
+template <int RD, int KD>
+void check_r32() {
+  typedef LdsTileR32<RD> L;
+  std::vector<int> seen(KD * RD, 0);
+  bool ok = true;
+  for (int k = 0; k < KD; k++)
+    for (int r = 0; r < RD; r++) {
+      const int o = L::off(k, r);
+      if (o < 0 || o >= KD * RD || seen[o]++) ok = false;
+    }
+  for (int s = 0; s < KD * RD / 4; s++) {
+    int k, r;
+    L::slot(s, k, r);
+    if (L::off(k, r) != s * 4) ok = false;
+  }
+  int worst = 0;
+  for (int r0 = 0; r0 < RD; r0 += 32)
+    for (int kk = 0; kk + 8 <= KD; kk += 8)
+      for (int t = 0; t < 4; t++) {
+        std::vector<std::pair<int, int>> acc;
+        for (int l = 0; l < 64; l++)
+          acc.push_back({4 * L::off(kk + 4 * (l >> 5) + t, r0 + (l & 31)), 4});
+        worst = std::max(worst, degree(acc));
+      }
+  printf("R32 %d %d %d %d\n", RD, KD, (int)ok, worst);
+}
+
 // K-major [ROWS][KD] tile read by ds_read_b128 fragments of an MI-row instruction
 template <int KD, int MI>
 void check_k() {
@@ -130,6 +160,7 @@ int main() {
   check_r<256, 64, 32, false>(); check_r<256, 128, 16, false>();
   check_r<64, 64, 32, true>();   check_r<128, 64, 32, true>();
   check_r<128, 128, 32, true>();
+  check_r32<64, 16>(); check_r32<128, 16>(); check_r32<256, 32>();
   check_k<32, 32>();  check_k<32, 16>();
   check_k<64, 32>();  check_k<64, 16>();
   check_k<128, 32>(); check_k<128, 16>();
@@ -157,6 +188,14 @@ def layout_report(tmp_path_factory):
 def test_r_major_tiles_are_bijective_and_conflict_free(layout_report):
     r = {k: v for k, v in layout_report.items() if k[0] == "R"}
     assert len(r) == 13
+    for key, (ok, worst) in r.items():
+        assert ok == 1, key
+        assert worst == 1, key
+
+
+def test_fp32_r_major_tiles_are_bijective_and_conflict_free(layout_report):
+    r = {k: v for k, v in layout_report.items() if k[0] == "R32"}
+    assert len(r) == 3
     for key, (ok, worst) in r.items():
         assert ok == 1, key
         assert worst == 1, key
