@@ -34,7 +34,9 @@ from . import hip as _hip
 # environment switches that change generated code (part of the specialization key)
 # Timing hook: None, or a callable returning the (start, stop) hipEvent_t
 # handles that the next launch's dispatch records at the kernel's start and end
-# (a benchmark sets it around its timed launches).
+# (a benchmark sets it around its timed launches). It is process-wide: while it
+# is set, every newt launch from any thread takes a pair, so set it only
+# around launches the timing code makes itself.
 launch_events = None
 
 _CODEGEN_ENV = ("NEWT_VEC", "NEWT_PIPELINE_DOT", "NEWT_LDS_DMA", "NEWT_MFMA", "NEWT_PID_REMAP",
