@@ -157,6 +157,9 @@ MATMUL_CONFIGS = [
     newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=3),
     newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=4, num_stages=4),
     newt.Config({"BLOCK_M": 64, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=3),
+    # 64x64 tiles give a 1024^3 problem 256 workgroups (one per CU)
+    newt.Config({"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 64}, num_warps=4, num_stages=4),
+    newt.Config({"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 64}, num_warps=4, num_stages=3),
 ]
 
 matmul_tuned = newt.autotune(configs=MATMUL_CONFIGS, key=["M", "N", "K"])(matmul_kernel)
