@@ -444,3 +444,20 @@ def test_sequential_pipelined_loops_share_lds_stages():
         assert lds == 64 * 1024
         assert len(re.findall(r"for \(; _it\d+ \+ 2 <", src)) == 2   # two fast copies
         assert src.count("newt::lds_dma16(") >= 16
+
+
+@pytest.mark.parametrize("cfg", [(256, 256, 16, 8, 3), (128, 128, 32, 4, 3)])
+def test_fp32_matmul_is_pipelined(cfg):
+    """fp32 operands take the pipelined k-loop: direct-to-LDS copies, the
+    branch-free fast copy, 16-byte fragment reads of the K-major A tile and
+    the full-precision fp32 MFMA."""
+    BM, BN, BK, nw, ns = cfg
+    src, lds = compile_source(W.matmul_kernel, _matmul_args(F32P),
+                              {"BLOCK_M": BM, "BLOCK_N": BN, "BLOCK_K": BK},
+                              num_warps=nw, num_stages=ns)
+    assert src.count("newt::lds_dma16(") > 0
+    assert re.search(r"for \(; _it\d+ \+ \d+ <", src)
+    assert "newt::lds_frag_k32f<" in src and "newt::LdsTileR32<" in src
+    assert lds == ns * (BM * BK + BK * BN) * 4
+    asm = isa(src)
+    assert "v_mfma_f32_32x32x2_f32" in asm and "ds_read_b128" in asm
