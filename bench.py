@@ -110,7 +110,7 @@ class _HipEvents:
             self.lib.hipEventDestroy(e)
 
 
-def timed_launches(fn, steps, embedded=True):
+def timed_launches(fn, steps, embedded=True, before=None):
     """Run fn() `steps` times back to back on the current stream (where newt
     launches) and time each launch with a HIP event pair. Returns (total ms
     between the first start and last end event, average ms of the per-launch
@@ -119,7 +119,11 @@ def timed_launches(fn, steps, embedded=True):
     embedded: fn makes exactly one newt launch, whose dispatch records the
     pair itself at the kernel's start and end (hipExtModuleLaunchKernel), so
     no event packets sit between the launches. Otherwise (a library call such
-    as torch.mm) the pair is recorded around each call."""
+    as torch.mm) the pair is recorded around each call.
+
+    before: called ahead of every fn() (a cache flush); with embedded timing
+    its own launches fall outside the pairs, which then hold the kernel's
+    execution on cold caches without the host's dispatch gap."""
     import torch
     from newt_amd.runtime import jit as J
     hev = _HipEvents()
@@ -136,16 +140,21 @@ def timed_launches(fn, steps, embedded=True):
                 raise RuntimeError("timed_launches: more than one newt launch per step")
             pos[0] = i + 1
             return pairs[i][0].value, pairs[i][1].value
-        J.launch_events = next_pair
         try:
             for i in range(steps):
+                if before is not None:
+                    before()
+                J.launch_events = next_pair
                 fn()
+                J.launch_events = None
         finally:
             J.launch_events = None
         if pos[0] != steps:
             raise RuntimeError("timed_launches: expected one newt launch per step")
     else:
         for i in range(steps):
+            if before is not None:
+                before()
             hev.record(st[i], stream)
             fn()
             hev.record(en[i], stream)
@@ -385,7 +394,7 @@ def warm_up(fn, seconds=0.03):
 def secondary():
     import torch
     from newt_amd import workloads as W
-    from newt_amd.testing import do_bench
+    from newt_amd.testing import _flush_buffer, do_bench
     res = []
     try:
         for name, work, fn, check in _secondary_workloads():
@@ -393,6 +402,9 @@ def secondary():
             warm_up(fn)
             ms = do_bench(fn, warmup=5, rep=20)        # caches flushed before each rep
             _, kern = timed_launches(fn, 20)            # back to back, per-launch events
+            flush = _flush_buffer()
+            # flushed like do_bench, timed by the dispatch's own events
+            _, kern_cold = timed_launches(fn, 20, before=lambda: flush.sum())
             if name.startswith("attention"):
                 res.append({"workload": name, "value": round(work / (ms * 1e-3) / 1e12, 2),
                             "unit": "TFLOP/s", "ms": round(ms, 5),
@@ -402,6 +414,9 @@ def secondary():
                 v = work / (ms * 1e-3) / 1e9
                 res.append({"workload": name, "value": round(v, 1), "unit": "GB/s",
                             "ms_flushed": round(ms, 5), "frac_hbm": round(v / PEAK_GBS, 4),
+                            "ms_kernel_flushed": round(kern_cold, 5),
+                            "frac_hbm_kernel_flushed": round(work / (kern_cold * 1e-3) / 1e9
+                                                             / PEAK_GBS, 4),
                             "ms_back_to_back": round(kern, 5), "bytes": work})
         from oracle import newt_oracle as orc
         # the other square sizes and dtypes of the matmul configuration, each
