@@ -342,7 +342,10 @@ class DotPipeline:
         ctx = (node, state, S, n, lo_e, stv, idt, slice_stmts, advance, skip, temps, kname, flat)
         if plan["fast_ok"] and os.environ.get("NEWT_PIPE_VERSION", "1") != "0":
             # leading iterations whose every tile is a whole in-bounds copy run
-            # in a copy of the loop with no per-iteration tests at all
+            # in a copy of the loop with no per-iteration tests at all; its
+            # copies take the buffer form (32-bit lane offsets) when every
+            # tile's lane offsets fit, which joins the entry test
+            state["bufdma"] = os.environ.get("NEWT_BUFFER_DMA", "1") != "0"
             nf = self._fast_count(ctx)
             self.emit(f"for (; {it0} + {2 * S - 2} < {nf.expr}; {it0} += {S}) {{")
             self._pipe_iterations(ctx, it0, fast=True)
@@ -453,6 +456,11 @@ class DotPipeline:
                 full = self.mask_all_true(X.mask, X.shape)
                 if full is not None and full != "true":
                     conds.append(f"({full})")
+                if full is not None and state.get("bufdma"):
+                    V = X if r["kdim"] == 1 else self.permute(X, (1, 0))
+                    lane = self._lane_bytes_fit(V, r["R"], r["K"], r["dt"])
+                    if lane != "true":
+                        conds.append(f"({lane})")
             X.consumed = True
             if X in self.pending_loads:
                 self.pending_loads.remove(X)
@@ -629,7 +637,7 @@ class DotPipeline:
             tile = f"(({dt.ctype}*)({base} + {r['off']}))"
             full = self.mask_all_true(X.mask, X.shape) if r["dma"] else None
             if r["dma"] and full is not None and fast:
-                self._dma_stage(V, base, r["off"], fmt, R, K, dt)
+                self._dma_stage(V, base, r["off"], fmt, R, K, dt, buffer=state.get("bufdma", False))
             elif fast:
                 self._reg_stage(V, tile, fmt, R, K, dt)
             elif r["dma"] and full is not None:
@@ -659,7 +667,30 @@ class DotPipeline:
         self.indent -= 1
         self.emit("}")
 
-    def _dma_stage(self, X, base, boff, fmt, R, K, dt):
+    def _lane_bytes_fit(self, V, R, K, dt):
+        """Uniform condition under which every lane's part of a DMA tile's
+        offset (c0 * r + c1 * k over the [R, K] view, without the tile's
+        uniform start) is a non-negative byte count below 2^31, as the buffer
+        form of the copy needs."""
+        off = V.ptr.offset
+        parts, conds = [], []
+        for c, ext in ((off.coefs.get(0), R - 1), (off.coefs.get(1), K - 1)):
+            if c is None:
+                continue
+            if c.is_const:
+                if c.const < 0:
+                    return "false"
+                parts.append(f"{c.const * ext}LL")
+            else:
+                conds.append(f"({c.expr}) >= 0")
+                parts.append(f"(long long)({c.expr}) * {ext}")
+        conds.append(f"({' + '.join(parts) if parts else '0LL'}) < {(1 << 31) // dt.itemsize}LL")
+        return " && ".join(conds)
+
+    def _dma_stage(self, X, base, boff, fmt, R, K, dt, buffer=False):
+        """Direct-to-LDS copies of one [R, K] tile. buffer: the branch-free
+        fast loop's form, a scalar descriptor on the tile's uniform start and
+        a 32-bit lane offset (the entry test guarantees it fits)."""
         off = X.ptr.offset
         T = dt.ctype
         epc = 16 // dt.itemsize
@@ -677,14 +708,21 @@ class DotPipeline:
                 self.emit(f"newt::LdsTileR32<{R}>::slot(_s, _k, _r);")
             else:
                 self.emit(f"newt::LdsTileR<{T}, {R}>::slot(_s, _k, _r);")
-            terms = [] if (off.base.is_const and off.base.const == 0) else [off.base.expr]
+            ubase = None if (off.base.is_const and off.base.const == 0) else off.base.expr
+            lane = []
             for c, v in ((c0, "_r"), (c1, "_k")):
                 if c is None:
                     continue
-                terms.append(v if c.is_const and c.const == 1 else f"{c.expr} * {v}")
-            gaddr = f"({gb} + {' + '.join(terms) if terms else '0'})"
+                lane.append(v if c.is_const and c.const == 1 else f"{c.expr} * {v}")
             dst = f"(void*)({base} + {boff} + {16 * i * self.T} + _wave * 1024)"
-            self.emit(f"newt::lds_dma16({gaddr}, {dst});")
+            if buffer:
+                tb = f"({gb} + ({ubase}))" if ubase else gb
+                lb = f"(unsigned)(({' + '.join(lane) if lane else '0'}) * {dt.itemsize})"
+                self.emit(f"newt::lds_dma16_buf({tb}, {lb}, {dst});")
+            else:
+                terms = ([ubase] if ubase else []) + lane
+                gaddr = f"({gb} + {' + '.join(terms) if terms else '0'})"
+                self.emit(f"newt::lds_dma16({gaddr}, {dst});")
             self.indent -= 1
             self.emit("}")
 

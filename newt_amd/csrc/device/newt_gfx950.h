@@ -417,6 +417,21 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* wave_dst) {
                                    (__attribute__((address_space(3))) void*)wave_dst, 16, 0, 0);
 }
 
+// The same copy from base + lane_bytes through a raw buffer descriptor
+// (buffer_load_dwordx4 ... offen lds). base must be the same for every lane
+// (it lives in scalar registers); lane_bytes is each lane's own 32-bit byte
+// offset, which stays in one VGPR across a loop where the 64-bit form needs a
+// VGPR pair and a 64-bit add per copy. Descriptor: stride 0, num_records
+// 0xFFFFFFFF (callers keep lane_bytes below 2^31, so the range check never
+// drops a lane), word 3 = 0x00020000 (32-bit data format, the raw-buffer word
+// of gfx9-family CDNA parts).
+__device__ __forceinline__ void lds_dma16_buf(const void* base, unsigned lane_bytes, void* wave_dst) {
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, -1, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)wave_dst, 16,
+                                           lane_bytes, 0, 0, 0);
+}
+
 // Wait until at most N vector-memory operations of this wave are outstanding
 // (s_waitcnt vmcnt(N); expcnt and lgkmcnt left unconstrained).
 template <int N>

@@ -40,7 +40,8 @@ from . import hip as _hip
 launch_events = None
 
 _CODEGEN_ENV = ("NEWT_VEC", "NEWT_PIPELINE_DOT", "NEWT_LDS_DMA", "NEWT_MFMA", "NEWT_PID_REMAP",
-                "NEWT_PIPE_VERSION", "NEWT_PLR", "NEWT_SCHED", "NEWT_HOIST_LOADS", "NEWT_PID_GROUP", "NEWT_IGLP")
+                "NEWT_PIPE_VERSION", "NEWT_PLR", "NEWT_SCHED", "NEWT_HOIST_LOADS", "NEWT_PID_GROUP", "NEWT_IGLP",
+                "NEWT_BUFFER_DMA")
 _CODEGEN_ENV_B = tuple(k.encode() for k in _CODEGEN_ENV)
 
 

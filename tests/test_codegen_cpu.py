@@ -461,3 +461,29 @@ def test_fp32_matmul_is_pipelined(cfg):
     assert lds == ns * (BM * BK + BK * BN) * 4
     asm = isa(src)
     assert "v_mfma_f32_32x32x2_f32" in asm and "ds_read_b128" in asm
+
+
+def test_fast_loop_copies_take_the_buffer_form(monkeypatch):
+    """In the branch-free fast loop each direct-to-LDS copy goes through a raw
+    buffer descriptor on the tile's uniform start plus a 32-bit lane offset
+    (buffer_load_dwordx4 ... offen lds): one loop-invariant VGPR per copy
+    instead of a VGPR pair and a 64-bit add. The loop is entered only when
+    every tile's lane offsets are non-negative and below 2^31 bytes; the
+    prologue and the general loop keep the 64-bit form, and
+    NEWT_BUFFER_DMA=0 turns the buffer form off."""
+    cex = {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}
+    src, _ = compile_source(W.matmul_kernel, _matmul_args(), cex, num_warps=4, num_stages=4)
+    loops = [m.start() for m in re.finditer(r"for \(; _it\d+ ", src)]
+    assert len(loops) == 2
+    before, fast, general = src[:loops[0]], src[loops[0]:loops[1]], src[loops[1]:]
+    assert fast.count("newt::lds_dma16_buf(") == 32 and "newt::lds_dma16(" not in fast
+    assert "lds_dma16_buf" not in before and "lds_dma16_buf" not in general
+    entry = before.rsplit("const int", 1)[1]
+    # fp16 lane offsets below 2^31 bytes: sam * 255 + 31 (A rows) and
+    # 255 + sbk * 31 (B rows) below 2^30 elements, strides non-negative
+    assert "(sam) >= 0" in entry and "(long long)(sam) * 255 + 31LL) < 1073741824LL" in entry
+    assert "(sbk) >= 0" in entry and "(255LL + (long long)(sbk) * 31) < 1073741824LL" in entry
+    assert re.search(r"buffer_load_dwordx4 v\d+, s\[\d+:\d+\], \S+ offen lds", isa(src))
+    monkeypatch.setenv("NEWT_BUFFER_DMA", "0")
+    src0, _ = compile_source(W.matmul_kernel, _matmul_args(), cex, num_warps=4, num_stages=4)
+    assert "lds_dma16_buf" not in src0 and "1073741824LL" not in src0

@@ -182,3 +182,46 @@ def test_matmul_fp32_is_full_precision():
     want = (a.double() @ b.double())
     rel = ((c.double() - want).norm() / want.norm()).item()
     assert rel < 1e-5
+
+
+
+# fp16 A rows whose lane offsets in a 256x32 tile, (sam * 255 + 31) * 2 bytes,
+# end just below / just above 2^31 (sam multiple of 16 either way)
+SAM_FITS, SAM_TOO_BIG = 4_210_688, 4_300_800
+
+
+@pytest.mark.parametrize("sam", [SAM_FITS, SAM_TOO_BIG])
+@pytest.mark.parametrize("buffer_dma", ["1", "0"])
+def test_lane_offsets_near_two_gib(sam, buffer_dma, monkeypatch):
+    """Rows of A 8.4 MB apart. Below the limit the fast loop's buffer-form
+    copies carry lane offsets up to ~2^31 bytes; above it the entry test
+    keeps every iteration on the general loop's 64-bit copies. Either way the
+    product is exact (a lane offset that wrapped would read the wrong rows of
+    the same allocation)."""
+    monkeypatch.setenv("NEWT_BUFFER_DMA", buffer_dma)
+    M = N = K = 256
+    flat = torch.empty(255 * sam + K, device="cuda", dtype=torch.float16)
+    a = flat.as_strided((M, K), (sam, 1))
+    a.copy_(rnd((M, K), torch.float16, 10))
+    b = rnd((K, N), torch.float16, 11)
+    c = torch.empty(M, N, device="cuda")
+    kloop_k2[(1, 1)](a, b, c, K, sam, BM=M, BN=N, BK=32, num_warps=4, num_stages=4)
+    want = a.float() @ b.float()
+    rel = ((c - want).norm() / want.norm()).item()
+    del flat, a
+    assert rel < 1e-3
+
+
+@newt.jit
+def kloop_k2(a_ptr, b_ptr, o_ptr, K, sam, BM: nl.constexpr, BN: nl.constexpr, BK: nl.constexpr):
+    rm, rn, rk = nl.arange(0, BM), nl.arange(0, BN), nl.arange(0, BK)
+    pa = a_ptr + rm[:, None] * sam + rk[None, :]
+    pb = b_ptr + rk[:, None] * BN + rn[None, :]
+    acc = nl.zeros((BM, BN), dtype=nl.float32)
+    for i in range(K // BK):
+        x = nl.load(pa)
+        y = nl.load(pb)
+        acc = nl.dot(x, y, acc)
+        pa += BK
+        pb += BK * BN
+    nl.store(o_ptr + rm[:, None] * BN + rn[None, :], acc)
