@@ -458,9 +458,11 @@ class DotPipeline:
                     conds.append(f"({full})")
                 if full is not None and state.get("bufdma"):
                     V = X if r["kdim"] == 1 else self.permute(X, (1, 0))
-                    lane = self._lane_bytes_fit(V, r["R"], r["K"], r["dt"])
-                    if lane != "true":
-                        conds.append(f"({lane})")
+                    conds.append(f"({self._lane_bytes_fit(V, r['R'], r['K'], r['dt'])})")
+                    if V is not X:
+                        V.consumed = True
+                        if V in self.pending_loads:
+                            self.pending_loads.remove(V)
             X.consumed = True
             if X in self.pending_loads:
                 self.pending_loads.remove(X)

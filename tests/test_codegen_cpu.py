@@ -478,6 +478,8 @@ def test_fast_loop_copies_take_the_buffer_form(monkeypatch):
     before, fast, general = src[:loops[0]], src[loops[0]:loops[1]], src[loops[1]:]
     assert fast.count("newt::lds_dma16_buf(") == 32 and "newt::lds_dma16(" not in fast
     assert "lds_dma16_buf" not in before and "lds_dma16_buf" not in general
+    # the entry test reads the tiles' offsets without emitting their loads
+    assert "? a_ptr[" not in fast and "? b_ptr[" not in fast
     entry = before.rsplit("const int", 1)[1]
     # fp16 lane offsets below 2^31 bytes: sam * 255 + 31 (A rows) and
     # 255 + sbk * 31 (B rows) below 2^30 elements, strides non-negative
