@@ -489,3 +489,28 @@ def test_fast_loop_copies_take_the_buffer_form(monkeypatch):
     monkeypatch.setenv("NEWT_BUFFER_DMA", "0")
     src0, _ = compile_source(W.matmul_kernel, _matmul_args(), cex, num_warps=4, num_stages=4)
     assert "lds_dma16_buf" not in src0 and "1073741824LL" not in src0
+
+
+def test_fast_loop_fills_are_spaced_evenly_over_the_mfmas():
+    """Interleave hints of the 4-wave 256x256x32 matmul's branch-free loop:
+    each stage's 64 MFMAs (one 32-deep k-step of a 128x128 wave tile) carry
+    its 8 copies and 24 next-stage fragment reads one after every second
+    MFMA, copies and reads alternating while both remain."""
+    src, _ = compile_source(W.matmul_kernel, _matmul_args(),
+                            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32},
+                            num_warps=4, num_stages=4)
+    loops = [m.start() for m in re.finditer(r"for \(; _it\d+ ", src)]
+    fast = src[loops[0]:loops[1]]
+    seq = re.findall(r"sched_group_barrier\((0x\w+), 1, 0\)", fast)
+    assert len(seq) == 4 * 96                       # 4 stages x (64 MFMAs + 32 fills)
+    first = seq[:96]
+    after = []
+    for mask in first:
+        if mask == "0x008":
+            after.append([])
+        else:
+            after[-1].append(mask)
+    assert len(after) == 64
+    assert [len(a) for a in after] == [1, 0] * 32
+    fills = [a[0] for a in after if a]
+    assert fills[:16] == ["0x020", "0x100"] * 8 and fills[16:] == ["0x100"] * 16
