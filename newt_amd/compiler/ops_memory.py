@@ -17,6 +17,8 @@ tiles take a per-run path (vector access when the run is fully valid,
 predicated element accesses otherwise).
 """
 
+import os
+
 from . import layouts as lo
 from . import types as tp
 from .codegen import CompileError
@@ -308,9 +310,23 @@ class MemoryOps:
         proven = pbase.aligned16 and div % chunk == 0
         all_true = self.mask_all_true(mask, L.shape)
         vd = self.cdtype(value)
+        # a matmul's C tile (a column-oriented dot accumulator: the kernel has
+        # no row reductions) is stored once, by every workgroup at about the
+        # same time, after its k-loop: the non-temporal hint keeps that burst
+        # from displacing operands that workgroups still in their k-loops read
+        # through L2 (4096^3 fp16: +0.3-4%). Attention's O (row-oriented,
+        # written as workgroups finish) measured 5-7% slower with it, and
+        # streaming row kernels slower too, so they keep plain stores.
+        acc = lo.mfma_tag_instr(L.tag)
+        nt = acc is not None and acc[1] == "col" and os.environ.get("NEWT_NT_STORE", "1") != "0"
 
         def val(s):
             return self.conv(self.ev(value, L, s), vd, elem)
+
+        def scalar_store(o, v):
+            if nt:
+                return f"__builtin_nontemporal_store(({elem.ctype})({v}), &{base}[{o}]);"
+            return f"{base}[{o}] = {v};"
 
         def body(masked):
             for g in range(0, L.nslots, chunk):
@@ -331,12 +347,12 @@ class MemoryOps:
                         conds.append(" && ".join(f"_m{i}" for i in range(chunk)))
                     if not proven:
                         conds.append(f"newt::aligned({addr}, {chunk * esz})")
-                    vec = f"newt::store_vec<{elem.ctype}, {chunk}>({addr}, _w);"
+                    vec = f"newt::store_vec{'_nt' if nt else ''}<{elem.ctype}, {chunk}>({addr}, _w);"
                     if conds:
                         self.emit(f"if ({' && '.join(conds)}) {{ {vec} }} else {{")
                         self.indent += 1
                         for i in range(chunk):
-                            st = f"{base}[{o} + {i}] = _w[{i}];"
+                            st = scalar_store(f"{o} + {i}", f"_w[{i}]")
                             self.emit(f"if (_m{i}) {st}" if masked else st)
                         self.indent -= 1
                         self.emit("}")
@@ -345,7 +361,7 @@ class MemoryOps:
                     self.indent -= 1
                     self.emit("}")
                 else:
-                    st = f"{base}[{o}] = {val(g)};"
+                    st = scalar_store(o, val(g))
                     if masked:
                         self.emit(f"if ({self.ev(mask, L, g)}) {st}")
                     else:

@@ -77,6 +77,18 @@ __device__ __forceinline__ void store_vec(T* __restrict__ p, const T* in) {
   *reinterpret_cast<R*>(p) = __builtin_bit_cast(R, v);
 }
 
+// store_vec with the non-temporal hint (global_store ... nt): for tiles written
+// once at the end of a long compute phase, whose lines should not displace the
+// operands other workgroups are still reading through L2.
+template <typename T, int N>
+__device__ __forceinline__ void store_vec_nt(T* __restrict__ p, const T* in) {
+  typedef typename raw_vec<sizeof(T) * N>::type R;
+  vec_t<T, N> v;
+#pragma unroll
+  for (int i = 0; i < N; ++i) v.d[i] = in[i];
+  __builtin_nontemporal_store(__builtin_bit_cast(R, v), reinterpret_cast<R*>(p));
+}
+
 __device__ __forceinline__ bool aligned(const void* p, int bytes) {
   return (reinterpret_cast<u64>(p) & (u64)(bytes - 1)) == 0;
 }

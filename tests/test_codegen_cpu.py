@@ -514,3 +514,36 @@ def test_fast_loop_fills_are_spaced_evenly_over_the_mfmas():
     assert [len(a) for a in after] == [1, 0] * 32
     fills = [a[0] for a in after if a]
     assert fills[:16] == ["0x020", "0x100"] * 8 and fills[16:] == ["0x100"] * 16
+
+
+def _attention_args():
+    args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
+    args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})
+    for n in ("sqb", "sqh", "sqm", "skb", "skh", "skn", "svb", "svh", "svn", "sob", "soh", "som"):
+        args[n] = (tp.int32, D16)
+    return args
+
+
+def test_matmul_tiles_are_stored_non_temporal(monkeypatch):
+    """A matmul's C tile (column-oriented dot accumulator) is stored with the
+    non-temporal hint (`global_store_short ... nt` on gfx950); attention's O
+    (row-oriented accumulator) and a streaming row kernel (softmax) keep
+    plain stores; NEWT_NT_STORE=0 turns the hint off."""
+    mm = lambda: compile_source(W.matmul_kernel, _matmul_args(),
+                                {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32},
+                                num_warps=4, num_stages=4)[0]
+    src = mm()
+    # 256 values per thread, in both the in-bounds and the masked branch
+    assert src.count("__builtin_nontemporal_store(") == 2 * 256 * 256 // 256
+    assert re.search(r"global_store_short v\[\d+:\d+\], v\d+, off nt", isa(src))
+    asrc, _ = compile_source(W.attention_kernel, _attention_args(),
+                             {"BLOCK_M": 128, "BLOCK_N": 64, "D": 128, "CAUSAL": False},
+                             num_warps=4, num_stages=2)
+    assert "newt::store_vec<__bf16, 4>(" in asrc and "nontemporal" not in asrc
+    assert "store_vec_nt" not in asrc
+    sm, _ = compile_source(W.softmax_kernel, {"x_ptr": (F32P, A16), "out_ptr": (F32P, A16),
+                                              "N": (tp.int32, D16), "stride": (tp.int32, D16)},
+                           {"BLOCK_N": 4096}, num_warps=4)
+    assert "nontemporal" not in sm and "store_vec_nt" not in sm
+    monkeypatch.setenv("NEWT_NT_STORE", "0")
+    assert "nontemporal" not in mm()
