@@ -1,24 +1,36 @@
-"""deuteron runtime: trace -> newt source -> correctness-gated autotune -> launch.
+"""deuteron runtime: specialise -> trace -> choose a configuration -> launch.
 
-Protocol of the reference (deuteron/runtime.py:1-311):
-  1. the kernel function run eagerly (full-size tiles = plain PyTorch) on
-     clones of the arguments is the correctness oracle;
-  2. the newt source is generated once per argument signature (ranks, dtypes);
-     tile sizes are constexprs, so every configuration reuses it;
-  3. candidate configurations are launched, wrong results rejected
-     (tolerance 2e-2 for half precision or dot kernels, else 1e-3), the rest
-     timed with do_bench: a seeded random sample, then up to three rounds of
-     neighbour search around the best;
-  4. the winner is cached in memory and in ~/.deuteron/configs.json
-     (DEUTERON_CACHE_DIR) under name:source-hash:pow2-shapes:dtypes.
+The protocol is the reference's (deuteron/runtime.py:47-311), which users
+and the examples rely on:
+  * the @dt.kernel function run eagerly (tiles span whole dimensions, every
+    dt.* call is plain PyTorch) on clones of the arguments is the oracle;
+  * the newt source is traced once per argument signature (ranks, dtypes,
+    scalar types); tile sizes are constexprs, so one source serves every
+    configuration;
+  * candidate configurations run on copies of the arguments, a result that
+    differs from the oracle (tolerance 2e-2 for half precision or dot
+    kernels, else 1e-3) disqualifies the configuration, the rest are timed
+    with do_bench: a seeded random sample of the space, then up to three
+    rounds of moves to neighbouring values around the best so far;
+  * the winner is kept in memory and in configs.json under
+    DEUTERON_CACHE_DIR (default ~/.deuteron), keyed
+    `name:source-hash:pow2-shapes:dtypes`.
 
-The search space is this backend's: tile sizes that map onto 32x32 MFMA tiles
-for dot kernels, num_warps counted in 64-wide waves, and num_stages for the
-software-pipelined k-loop. Dot kernels try a few known-good gfx950 tilings
-before the random sample.
+Structure (this backend's own):
+  _Specialization  one traced kernel for one argument signature: its newt
+                   JIT function, the extents it reads from the arguments and
+                   the launch (grid, constexprs, flattened arguments)
+  SearchSpace      the configurations worth trying for a traced kernel on
+                   gfx950: MFMA-sized tiles and pipeline depths for dot
+                   kernels, tile footprints that fit a workgroup otherwise
+  Tuner            the correctness-gated search, with a log of its trials
+  ConfigStore      configs.json, updated under a file lock and replaced
+                   atomically so an interrupted or concurrent writer never
+                   leaves a truncated file or drops another key's entry
 """
 
 import ast
+import contextlib
 import hashlib
 import inspect
 import itertools
@@ -26,6 +38,7 @@ import json
 import linecache
 import os
 import random
+import tempfile
 import textwrap
 
 import torch
@@ -33,275 +46,404 @@ import torch
 from . import tracer
 from .language import EagerTensor
 
-_DOT_BLOCKS = [32, 64, 128, 256]
-_ELT_BLOCKS = [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096]
+_DOT_TILES = (32, 64, 128, 256)
+_ELT_TILES = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096)
+# largest tile footprint (elements per program) tried for kernels without a dot
+_ELT_FOOTPRINT = 1 << 15
+# gfx950 tilings dot kernels start from: (grid tile, inner tile, waves, stages)
+_DOT_SEEDS = ((256, 32, 4, 4), (256, 32, 8, 4), (128, 64, 4, 3), (128, 32, 4, 4))
 
 
-def _cache_file():
-    d = os.environ.get("DEUTERON_CACHE_DIR") or os.path.join(os.path.expanduser("~"), ".deuteron")
-    os.makedirs(d, exist_ok=True)
-    return os.path.join(d, "configs.json")
-
-
-def _pow2(n):
+def _pow2_at_least(n):
     n = int(n)
     return 1 if n <= 1 else 1 << (n - 1).bit_length()
 
 
 class Config(dict):
-    """A configuration: BLOCK_<TILE> sizes plus num_warps / num_stages."""
+    """A configuration: the BLOCK_<TILE> sizes plus num_warps and
+    num_stages (absent: 4 waves, 3 stages)."""
 
     @property
     def num_warps(self):
         return self.get("num_warps", 4)
 
+    @property
+    def num_stages(self):
+        return self.get("num_stages", 3)
+
+    def frozen(self):
+        return frozenset(self.items())
+
+
+# ------------------------------------------------------------------ specialisation
+
+def _load_source(kernel_name, traced):
+    """Execute the traced module and return its @newt.jit function. newt
+    reads kernel text with inspect.getsource, so the text is registered
+    with linecache under a name unique to the source."""
+    digest = hashlib.sha256(traced.source.encode()).hexdigest()
+    fname = f"<deuteron {kernel_name} {digest[:12]}>"
+    linecache.cache[fname] = (len(traced.source), None, traced.source.splitlines(True), fname)
+    namespace = {}
+    exec(compile(traced.source, fname, "exec"), namespace)
+    return namespace[traced.name], digest[:12]
+
+
+class _Specialization:
+    def __init__(self, kernel, args):
+        self.traced = tracer.generate(kernel.fn, kernel.fndef, args)
+        self.jit, self.digest = _load_source(kernel.__name__, self.traced)
+        self.index = {name: i for i, name in enumerate(kernel.param_names)}
+
+    def extents(self, args):
+        out = {}
+        for entry in self.traced.args:
+            value = args[self.index[entry[1]]]
+            if entry[0] == "tensor":
+                for axis, size in enumerate(value.shape):
+                    out[f"{entry[1]}_d{axis}"] = int(size)
+            else:
+                out[entry[1]] = value
+        return out
+
+    @staticmethod
+    def resolve(extents, symbol):
+        return int(extents[symbol]) if symbol in extents else int(symbol)
+
+    def flat_args(self, args):
+        out = []
+        for entry in self.traced.args:
+            value = args[self.index[entry[1]]]
+            out.append(value)
+            if entry[0] == "tensor":
+                out.extend(int(s) for s in value.shape)
+                out.extend(int(s) for s in value.stride())
+        return out
+
+    def span_sizes(self, extents):
+        """Constexprs of whole-dimension tiles; the dimensions one tile spans
+        must agree (x[t, :] * w[:] needs x.shape[1] == w.shape[0])."""
+        out = {}
+        for const, symbols in self.traced.spans:
+            sizes = {self.resolve(extents, s) for s in symbols}
+            if len(sizes) != 1:
+                raise ValueError(f"deuteron: dimensions {', '.join(symbols)} meet in one "
+                                 f"expression but have sizes {sorted(sizes)}")
+            out[const] = _pow2_at_least(sizes.pop())
+        return out
+
+    def launch(self, args, cfg):
+        extents = self.extents(args)
+        consts = {name: cfg[name] for name in self.traced.tunable}
+        consts.update(self.span_sizes(extents))
+        grid = tuple(-(-self.resolve(extents, d.extent) // consts[d.const])
+                     for d in self.traced.grid)
+        self.jit[grid](*self.flat_args(args), **consts, num_warps=cfg.num_warps,
+                       num_stages=cfg.num_stages)
+
+
+# ------------------------------------------------------------------ search space
+
+class SearchSpace:
+    """Values per configuration knob for one traced kernel at one problem."""
+
+    def __init__(self, traced, span_elements=1):
+        self.dot = traced.has_dot
+        self.grid_consts = {d.const for d in traced.grid}
+        self.tiles = list(traced.tunable)
+        self.values = {name: list(_DOT_TILES if self.dot else _ELT_TILES) for name in self.tiles}
+        self.values["num_warps"] = [2, 4, 8] if self.dot else [1, 2, 4, 8]
+        if self.dot:
+            self.values["num_stages"] = [2, 3, 4]
+        self.span_elements = span_elements
+
+    def admits(self, cfg):
+        if any(cfg.get(k) not in opts for k, opts in self.values.items()):
+            return False
+        if self.dot:
+            return True
+        footprint = self.span_elements
+        for name in self.tiles:
+            footprint *= cfg[name]
+        return footprint <= _ELT_FOOTPRINT
+
+    def every(self):
+        names = list(self.values)
+        combos = (Config(zip(names, vals)) for vals in itertools.product(*self.values.values()))
+        return [c for c in combos if self.admits(c)]
+
+    def seeds(self):
+        """Known-good gfx950 tilings mapped onto this kernel's tiles: grid
+        tiles take the output-tile size, inner (k) tiles the k-step."""
+        if not self.dot:
+            return []
+        out = []
+        for grid_tile, inner_tile, warps, stages in _DOT_SEEDS:
+            cfg = Config(num_warps=warps, num_stages=stages)
+            for name in self.tiles:
+                cfg[name] = grid_tile if name in self.grid_consts else inner_tile
+            if self.admits(cfg):
+                out.append(cfg)
+        return out
+
+    def default(self):
+        seeds = self.seeds()
+        if seeds:
+            return seeds[0]
+        cfg = Config(num_warps=4)
+        for name in self.tiles:
+            cfg[name] = 1
+        for size in reversed(self.values[self.tiles[0]] if self.tiles else []):
+            for name in self.tiles:
+                cfg[name] = size if name == self.tiles[0] else 1
+            if self.admits(cfg):
+                break
+        return cfg
+
+    def moves(self, cfg):
+        """Configurations one step away from cfg along one knob."""
+        out = []
+        for knob, opts in self.values.items():
+            i = opts.index(cfg[knob]) if cfg.get(knob) in opts else 0
+            for j in (i - 1, i + 1):
+                if 0 <= j < len(opts):
+                    moved = Config(cfg)
+                    moved[knob] = opts[j]
+                    if self.admits(moved):
+                        out.append(moved)
+        return out
+
+
+# ------------------------------------------------------------------ tuning
+
+class Tuner:
+    """Runs candidate configurations on copies of the arguments, checks them
+    against the eager oracle and times the correct ones."""
+
+    def __init__(self, kernel, spec, args):
+        self.kernel, self.spec = kernel, spec
+        self.trials = []          # (Config, ms or None, note)
+        names = kernel.param_names
+        clones = [a.clone() if torch.is_tensor(a) else a for a in args]
+        kernel._eager(clones)
+        writes = spec.traced.writes
+        self.expected = {n: clones[names.index(n)] for n in writes}
+        self.work = [a.clone() if torch.is_tensor(a) else a for a in args]
+        self.initial = {n: args[names.index(n)] for n in writes}
+        self.outputs = {n: self.work[names.index(n)] for n in writes}
+
+    def tolerance(self, t):
+        return 2e-2 if (t.dtype in (torch.float16, torch.bfloat16) or self.spec.traced.has_dot) \
+            else 1e-3
+
+    def evaluate(self, cfg):
+        from newt_amd.testing import do_bench
+
+        for name, out in self.outputs.items():
+            out.copy_(self.initial[name])
+        try:
+            self.spec.launch(self.work, cfg)
+            torch.cuda.synchronize()
+        except Exception as exc:   # a configuration the compiler or the launch rejects
+            return self._log(cfg, None, f"invalid: {str(exc).splitlines()[0][:100]}")
+        for name, want in self.expected.items():
+            tol = self.tolerance(want)
+            if not torch.allclose(self.outputs[name].float(), want.float(), rtol=tol, atol=tol):
+                return self._log(cfg, None, "wrong result")
+        ms = do_bench(lambda: self.spec.launch(self.work, cfg), warmup=3, rep=10)
+        return self._log(cfg, ms, "")
+
+    def _log(self, cfg, ms, note):
+        self.trials.append((cfg, ms, note))
+        if self.kernel.verbose:
+            print(f"  {dict(cfg)}: {f'{ms:.4f} ms' if ms is not None else note}")
+        return ms
+
+    def search(self, space, samples):
+        tried = set()
+
+        def run(cfg):
+            if cfg.frozen() in tried:
+                return None
+            tried.add(cfg.frozen())
+            return self.evaluate(cfg)
+
+        every = space.every()
+        sample = every if len(every) <= samples else random.Random(0).sample(every, samples)
+        best, best_ms = None, float("inf")
+        for cfg in space.seeds() + sample:
+            ms = run(cfg)
+            if ms is not None and ms < best_ms:
+                best, best_ms = cfg, ms
+        if best is None:
+            raise RuntimeError(f"deuteron: no configuration of {self.kernel.__name__} ran "
+                               f"correctly (DEUTERON_VERBOSE=1 lists the trials)")
+        for _ in range(3):
+            step = None
+            for cfg in space.moves(best):
+                ms = run(cfg)
+                if ms is not None and ms < best_ms:
+                    step, best_ms = cfg, ms
+            if step is None:
+                break
+            best = step
+        if self.kernel.verbose:
+            print(f"deuteron: {self.kernel.__name__} -> {dict(best)} ({best_ms:.4f} ms)")
+        return best
+
+
+# ------------------------------------------------------------------ persistence
+
+class ConfigStore:
+    """configs.json in DEUTERON_CACHE_DIR (default ~/.deuteron)."""
+
+    @staticmethod
+    def directory():
+        return os.environ.get("DEUTERON_CACHE_DIR") or os.path.join(os.path.expanduser("~"),
+                                                                    ".deuteron")
+
+    def path(self):
+        return os.path.join(self.directory(), "configs.json")
+
+    def read(self):
+        try:
+            with open(self.path()) as f:
+                data = json.load(f)
+            return data if isinstance(data, dict) else {}
+        except (OSError, ValueError):
+            return {}
+
+    def get(self, key):
+        entry = self.read().get(key)
+        return Config(entry) if isinstance(entry, dict) else None
+
+    @contextlib.contextmanager
+    def _locked(self):
+        import fcntl
+        os.makedirs(self.directory(), exist_ok=True)
+        with open(self.path() + ".lock", "a") as lock:
+            fcntl.flock(lock, fcntl.LOCK_EX)
+            try:
+                yield
+            finally:
+                fcntl.flock(lock, fcntl.LOCK_UN)
+
+    def put(self, key, cfg):
+        """Add one entry: re-read the file under the lock (other processes
+        may have added keys), write the merge to a temporary file in the
+        same directory and rename it over configs.json."""
+        try:
+            with self._locked():
+                data = self.read()
+                data[key] = dict(cfg)
+                fd, tmp = tempfile.mkstemp(prefix=".configs-", suffix=".json",
+                                           dir=self.directory())
+                try:
+                    with os.fdopen(fd, "w") as f:
+                        json.dump(data, f, indent=1, sort_keys=True)
+                    os.replace(tmp, self.path())
+                except BaseException:
+                    with contextlib.suppress(OSError):
+                        os.unlink(tmp)
+                    raise
+        except OSError:
+            pass    # a read-only cache directory only costs a re-tune next time
+
+
+_STORE = ConfigStore()
+
+
+# ------------------------------------------------------------------ the kernel object
 
 class Kernel:
+    """A @dt.kernel function: call it with tensors (and numbers) to trace,
+    tune (once per problem class) and launch it on the GPU."""
+
     def __init__(self, fn, config=None, autotune=True, samples=12, verbose=False):
         self.fn = fn
         self.__name__ = fn.__name__
         self.fndef = ast.parse(textwrap.dedent(inspect.getsource(fn))).body[0]
+        self.param_names = [a.arg for a in self.fndef.args.args]
         self.fixed_config = Config(config) if config else None
         self.autotune_enabled = autotune and config is None
         self.samples = samples
         self.verbose = verbose or bool(os.environ.get("DEUTERON_VERBOSE"))
-        self._ks = None
-        self._ks_sig = None
-        self._jit = None
-        self._configs = {}
+        self.trials = []        # the latest tuning's (Config, ms or None, note)
+        self._specs = {}        # argument signature -> _Specialization
+        self._chosen = {}       # tuning key -> Config
+        self._last = None
 
-    # ------------------------------------------------------------ public API
+    # ---- public API
     def __call__(self, *args):
         if os.environ.get("DEUTERON_INTERPRET"):
             return self._eager(args)
-        ks = self._source_for(args)
-        cfg = self.fixed_config or self._get_config(ks, args)
-        self._launch(ks, args, cfg)
+        spec = self._specialize(args)
+        cfg = self.fixed_config or self._choose(spec, args)
+        self._last = cfg
+        spec.launch(args, cfg)
 
     def ref(self, *args):
-        """Run the eager PyTorch reference (the oracle)."""
+        """Run the eager PyTorch form of the kernel (the oracle)."""
         return self._eager(args)
 
     def to_newt_source(self, *args):
-        """The generated newt kernel source for these example arguments."""
-        return self._source_for(args).source
+        """The newt kernel source traced for these example arguments."""
+        return self._specialize(args).traced.source
 
     @property
     def best_config(self):
-        vals = list(self._configs.values())
-        return vals[-1] if vals else self.fixed_config
+        """The configuration of the latest launch (or the fixed one)."""
+        return self._last or self.fixed_config
 
-    # ------------------------------------------------------------- internals
+    # ---- internals
     def _eager(self, args):
         return self.fn(*[EagerTensor(a) if torch.is_tensor(a) else a for a in args])
 
-    @staticmethod
-    def _signature(args):
-        return tuple((a.dim(), str(a.dtype)) if torch.is_tensor(a) else type(a).__name__
-                     for a in args)
-
-    def _source_for(self, args):
-        sig = self._signature(args)
-        if self._ks is None or self._ks_sig != sig:
-            ks = tracer.generate(self.fn, self.fndef, args)
-            fname = f"<deuteron:{self.__name__}:{hashlib.sha256(ks.source.encode()).hexdigest()[:8]}>"
-            # newt reads kernel source with inspect.getsource: register it
-            linecache.cache[fname] = (len(ks.source), None, ks.source.splitlines(True), fname)
-            ns = {}
-            exec(compile(ks.source, fname, "exec"), ns)
-            self._ks, self._ks_sig, self._jit = ks, sig, ns[ks.name]
+    def _specialize(self, args):
+        sig = tuple((a.dim(), str(a.dtype)) if torch.is_tensor(a) else type(a).__name__
+                    for a in args)
+        spec = self._specs.get(sig)
+        if spec is None:
+            spec = self._specs[sig] = _Specialization(self, args)
             if self.verbose:
-                print(f"=== deuteron: generated newt source for {self.__name__} ===")
-                print(ks.source)
-        return self._ks
+                print(f"=== deuteron: newt source of {self.__name__} ===\n{spec.traced.source}")
+        return spec
 
-    def _sizes(self, ks, args):
-        by = dict(zip([a.arg for a in self.fndef.args.args], args))
-        sizes = {}
-        for kind, nm in ks.params:
-            if kind == "tensor":
-                for d, s in enumerate(by[nm].shape):
-                    sizes[f"{nm}_d{d}"] = int(s)
-            else:
-                sizes[nm] = by[nm]
-        return sizes
-
-    def _args(self, ks, args):
-        by = dict(zip([a.arg for a in self.fndef.args.args], args))
-        out = []
-        for kind, nm in ks.params:
-            v = by[nm]
-            out.append(v)
-            if kind == "tensor":
-                out += [int(s) for s in v.shape] + [int(s) for s in v.stride()]
-        return out
-
-    @staticmethod
-    def _size(sizes, sym):
-        return int(sizes[sym]) if sym in sizes else int(sym)
-
-    def _constexprs(self, ks, sizes, cfg):
-        return {td.block: (_pow2(self._size(sizes, td.size)) if td.kind == "full" else cfg[td.block])
-                for td in ks.tile_vars}
-
-    def _launch(self, ks, args, cfg):
-        sizes = self._sizes(ks, args)
-        kw = self._constexprs(ks, sizes, cfg)
-        grid = tuple(-(-self._size(sizes, td.size) // kw[td.block]) for td in ks.grid_tiles)
-        self._jit[grid](*self._args(ks, args), **kw, num_warps=cfg.num_warps,
-                        num_stages=cfg.get("num_stages", 3))
-
-    # ------------------------------------------------------------ autotuning
-    def _key(self, ks, args):
-        h = getattr(ks, "_hash", None)
-        if h is None:
-            h = ks._hash = hashlib.sha256(ks.source.encode()).hexdigest()[:12]
-        shapes = tuple(tuple(_pow2(s) for s in a.shape) if torch.is_tensor(a) else None
+    def tuning_key(self, spec, args):
+        shapes = tuple(tuple(_pow2_at_least(s) for s in a.shape) if torch.is_tensor(a) else None
                        for a in args)
-        dts = tuple(str(a.dtype) if torch.is_tensor(a) else "" for a in args)
-        return f"{self.__name__}:{h}:{shapes}:{dts}"
+        dtypes = tuple(str(a.dtype) if torch.is_tensor(a) else "" for a in args)
+        return f"{self.__name__}:{spec.digest}:{shapes}:{dtypes}"
 
-    def _get_config(self, ks, args):
-        key = self._key(ks, args)
-        cfg = self._configs.get(key)
-        if cfg is not None:
-            return cfg
-        try:
-            with open(_cache_file()) as f:
-                disk = json.load(f)
-        except (OSError, ValueError):
-            disk = {}
-        if key in disk:
-            cfg = Config(disk[key])
-        else:
-            cfg = self._autotune(ks, args)
-            disk[key] = dict(cfg)
-            try:
-                with open(_cache_file(), "w") as f:
-                    json.dump(disk, f, indent=1)
-            except OSError:
-                pass
-        self._configs[key] = cfg
+    def _space(self, spec, args):
+        spans = spec.span_sizes(spec.extents(args))
+        footprint = 1
+        for size in spans.values():
+            footprint *= size
+        return SearchSpace(spec.traced, footprint)
+
+    def _choose(self, spec, args):
+        key = self.tuning_key(spec, args)
+        cfg = self._chosen.get(key)
+        if cfg is None:
+            cfg = _STORE.get(key)
+            if cfg is None:
+                space = self._space(spec, args)
+                if self.autotune_enabled:
+                    tuner = Tuner(self, spec, args)
+                    cfg = tuner.search(space, self.samples)
+                    self.trials = tuner.trials
+                    _STORE.put(key, cfg)
+                else:
+                    cfg = space.default()       # untuned: not worth persisting
+            self._chosen[key] = cfg
         return cfg
-
-    @staticmethod
-    def _has_dot(ks):
-        return "nl.dot(" in ks.source
-
-    def _space(self, ks):
-        dot = self._has_dot(ks)
-        space = {nm: (_DOT_BLOCKS if dot else _ELT_BLOCKS) for nm in ks.tunable}
-        space["num_warps"] = [2, 4, 8] if dot else [1, 2, 4, 8]
-        if dot:
-            space["num_stages"] = [2, 3, 4]
-        return space
-
-    @staticmethod
-    def _priors(ks, space):
-        """Configurations tried before the random sample for dot kernels: the
-        tiles gfx950 matmuls run best with (256x256 or 128x128 output tiles,
-        k-tiles of 32/64, 4 or 8 waves, 3-4 stages), mapped onto this kernel's
-        grid tiles and inner (k) tiles."""
-        if "num_stages" not in space:
-            return []
-        grid = {td.block for td in ks.grid_tiles}
-        out = []
-        for g, kt, nw, ns in ((256, 32, 4, 4), (256, 32, 8, 4), (128, 64, 4, 3), (128, 32, 4, 4)):
-            cfg = Config(num_warps=nw, num_stages=ns)
-            for nm in ks.tunable:
-                cfg[nm] = g if nm in grid else kt
-            if all(cfg[k] in space[k] for k in space):
-                out.append(cfg)
-        return out
-
-    @staticmethod
-    def _neighbours(cfg, space):
-        out = []
-        for k, opts in space.items():
-            i = opts.index(cfg[k]) if cfg[k] in opts else 0
-            for j in (i - 1, i + 1):
-                if 0 <= j < len(opts):
-                    n = Config(cfg)
-                    n[k] = opts[j]
-                    out.append(n)
-        return out
-
-    def _autotune(self, ks, args):
-        from newt_amd.testing import do_bench
-
-        space = self._space(ks)
-        names = [a.arg for a in self.fndef.args.args]
-        # the oracle: the function run eagerly on clones
-        oracle = [a.clone() if torch.is_tensor(a) else a for a in args]
-        self._eager(oracle)
-        expected = {p: dict(zip(names, oracle))[p].clone() for p in ks.store_params}
-        work = [a.clone() if torch.is_tensor(a) else a for a in args]
-        outs = {p: dict(zip(names, work))[p] for p in ks.store_params}
-        initial = {p: dict(zip(names, args))[p] for p in ks.store_params}
-        dot = self._has_dot(ks)
-
-        def tol(t):
-            return 2e-2 if (t.dtype in (torch.float16, torch.bfloat16) or dot) else 1e-3
-
-        def attempt(cfg):
-            for p, o in outs.items():
-                o.copy_(initial[p])
-            try:
-                self._launch(ks, work, cfg)
-                torch.cuda.synchronize()
-            except Exception as e:  # invalid configuration (too much LDS, ...)
-                if self.verbose:
-                    print(f"  {dict(cfg)}: invalid ({str(e).splitlines()[0][:100]})")
-                return None
-            for p, want in expected.items():
-                t = tol(want)
-                if not torch.allclose(outs[p].float(), want.float(), rtol=t, atol=t):
-                    if self.verbose:
-                        print(f"  {dict(cfg)}: WRONG RESULT (skipped)")
-                    return None
-            ms = do_bench(lambda: self._launch(ks, work, cfg), warmup=3, rep=10)
-            if self.verbose:
-                print(f"  {dict(cfg)}: {ms:.4f} ms")
-            return ms
-
-        keys = list(space)
-        every = [Config(zip(keys, vals)) for vals in itertools.product(*[space[k] for k in keys])]
-        rng = random.Random(0)
-        cands = every if len(every) <= self.samples else rng.sample(every, self.samples)
-        cands = self._priors(ks, space) + cands
-        seen, results = set(), []
-        for cfg in cands:
-            sig = frozenset(cfg.items())
-            if sig in seen:
-                continue
-            seen.add(sig)
-            ms = attempt(cfg)
-            if ms is not None:
-                results.append((ms, cfg))
-        if not results:
-            raise RuntimeError(f"deuteron: no valid config found for {self.__name__} "
-                               f"(try DEUTERON_VERBOSE=1)")
-        best_ms, best = min(results, key=lambda r: r[0])
-        for _ in range(3):
-            improved = False
-            for n in self._neighbours(best, space):
-                sig = frozenset(n.items())
-                if sig in seen:
-                    continue
-                seen.add(sig)
-                ms = attempt(n)
-                if ms is not None and ms < best_ms:
-                    best_ms, best, improved = ms, n, True
-            if not improved:
-                break
-        if self.verbose:
-            print(f"deuteron: {self.__name__} best {dict(best)} = {best_ms:.4f} ms")
-        return best
 
 
 def kernel(fn=None, *, config=None, autotune=True, samples=12, verbose=False):
-    """@deuteron.kernel: compile a tile-DSL function to autotuned newt kernels."""
+    """@deuteron.kernel, or @deuteron.kernel(config=..., autotune=...,
+    samples=..., verbose=...): compile a tile-DSL function to newt kernels."""
     if fn is None:
         return lambda f: Kernel(f, config=config, autotune=autotune, samples=samples,
                                 verbose=verbose)
-    return Kernel(fn)
+    return Kernel(fn, config=config, autotune=autotune, samples=samples, verbose=verbose)

@@ -1,134 +1,184 @@
-"""@newt.autotune / @newt.heuristics (reference newt/runtime/autotuner.py:5-128).
+"""Launch-time choice of constexprs: @newt.autotune and @newt.heuristics.
 
-Same protocol as the reference: each config is timed with do_bench, configs
-that fail to compile or launch are skipped, the fastest is cached per key
-(values of the `key` arguments, shapes for tensors, plus every tensor's dtype),
-`reset_to_zero` arguments are zeroed before every timed run and once more
-before the real launch after tuning. Configs that would need more LDS than
-gfx950 has fail at compile time and are skipped like any invalid config.
+Observable behaviour matches the reference decorators
+(newt/runtime/autotuner.py:5-128), which existing kernels rely on:
+  * a tuning key of the `key` arguments' values (a tensor contributes its
+    shape) followed by the dtype of every tensor argument;
+  * on the first launch for a key every Config is timed with do_bench (cache
+    flushed between repetitions); a Config that fails to compile or launch
+    (too much LDS, a tiling the compiler rejects, ...) is dropped, and when
+    none is left the launch raises RuntimeError chained to the last failure;
+  * `reset_to_zero` tensors are cleared before every timed run and once more
+    before the real launch that follows tuning, so a read-modify-write
+    kernel does not see the tuning runs' partial results;
+  * the winner is kept per key for the life of the process, and
+    `best_config` names the Config of the latest launch.
+
+The structure here is this backend's own: a launch binds its arguments once
+(`_Binding`), tuning is a separate step that returns a ranked `Tuning`
+record (kept in `timings` / `failures` for inspection), and the launch itself
+is a single merge of the call's keyword arguments with the chosen Config.
 """
+
+import functools
 
 
 class Config:
+    """One candidate launch of a kernel: constexpr values plus num_warps
+    (64-wide waves per workgroup on gfx950) and num_stages (depth of the
+    dot pipeline). Equal Configs hash equal, so they can key dictionaries."""
+
+    __slots__ = ("kwargs", "num_warps", "num_stages")
+
     def __init__(self, kwargs, num_warps=4, num_stages=1):
         self.kwargs = dict(kwargs)
         self.num_warps = num_warps
         self.num_stages = num_stages
 
     def all_kwargs(self):
-        return {**self.kwargs, "num_warps": self.num_warps, "num_stages": self.num_stages}
+        """The keyword arguments a launch with this Config passes."""
+        out = dict(self.kwargs)
+        out["num_warps"] = self.num_warps
+        out["num_stages"] = self.num_stages
+        return out
+
+    def _identity(self):
+        return (tuple(sorted(self.kwargs.items())), self.num_warps, self.num_stages)
+
+    def __eq__(self, other):
+        return isinstance(other, Config) and self._identity() == other._identity()
+
+    def __hash__(self):
+        return hash(self._identity())
 
     def __repr__(self):
-        kw = ", ".join(f"{k}={v}" for k, v in self.kwargs.items())
-        return f"Config({kw}, num_warps={self.num_warps})"
+        # the reference's text: constexprs then num_warps (stages not shown)
+        inner = [f"{k}={v}" for k, v in self.kwargs.items()]
+        inner.append(f"num_warps={self.num_warps}")
+        return "Config(" + ", ".join(inner) + ")"
+
+
+class _Binding:
+    """One call's arguments by parameter name, the kernel's defaults filled
+    in where the call leaves them out."""
+
+    def __init__(self, fn, args, kwargs):
+        values = dict(zip(fn.param_names, args))
+        values.update(kwargs)
+        for name, default in getattr(fn, "defaults", {}).items():
+            values.setdefault(name, default)
+        self.values = values
+
+    def tuning_key(self, key_names):
+        import torch
+
+        def part(v):
+            return tuple(v.shape) if hasattr(v, "shape") else v
+        head = tuple(part(self.values.get(name)) for name in key_names)
+        dtypes = tuple(str(v.dtype) for v in self.values.values() if isinstance(v, torch.Tensor))
+        return head + dtypes
+
+    def zero(self, names):
+        for name in names:
+            self.values[name].zero_()
+
+
+class Tuning:
+    """The outcome of tuning one key: (ms, Config) fastest first, and the
+    Configs that could not run with the error each raised."""
+
+    def __init__(self):
+        self.ranked = []
+        self.failed = []
+
+    @property
+    def best(self):
+        return self.ranked[0][1]
 
 
 class Autotuner:
+    """A JIT function launched with the fastest of `configs` per tuning key."""
+
     def __init__(self, jitfn, configs, key, reset_to_zero=None, warmup=5, rep=20):
         self.jitfn = jitfn
-        self.configs = configs
-        self.key = key
-        self.reset_to_zero = reset_to_zero or []
+        self.configs = list(configs)
+        self.key = list(key)
+        self.reset_to_zero = list(reset_to_zero or [])
         self.warmup = warmup
         self.rep = rep
-        self.cache = {}
+        self.cache = {}        # tuning key -> Config
+        self.timings = {}      # tuning key -> [(ms, Config)], fastest first
+        self.failures = {}     # tuning key -> [(Config, exception)]
         self.best_config = None
-        self.timings = {}
         self.__name__ = getattr(jitfn, "__name__", "kernel")
         self.param_names = getattr(jitfn, "param_names", [])
         self.defaults = getattr(jitfn, "defaults", {})
 
     def __getitem__(self, grid):
-        def runner(*args, **kwargs):
-            return self._run(grid, args, kwargs)
+        return functools.partial(self._launch, grid)
 
-        return runner
+    def _launch_with(self, grid, args, kwargs, cfg):
+        merged = dict(kwargs)
+        merged.update(cfg.all_kwargs())
+        return self.jitfn[grid](*args, **merged)
 
-    def _key_values(self, args, kwargs):
-        import torch
-
-        bound = dict(zip(self.jitfn.param_names, args))
-        bound.update(kwargs)
-        for n, d in getattr(self.jitfn, "defaults", {}).items():
-            bound.setdefault(n, d)
-        vals = []
-        for k in self.key:
-            v = bound.get(k)
-            vals.append(tuple(v.shape) if hasattr(v, "shape") else v)
-        for v in bound.values():
-            if isinstance(v, torch.Tensor):
-                vals.append(str(v.dtype))
-        return tuple(vals)
-
-    def _run(self, grid, args, kwargs):
+    def tune(self, grid, args, kwargs, binding):
+        """Time every Config on this call's arguments; a Tuning record."""
         from ..testing import do_bench
 
-        keyv = self._key_values(args, kwargs)
-        bound = dict(zip(self.jitfn.param_names, args))
-        bound.update(kwargs)
-        best = self.cache.get(keyv)
-        tuned_now = False
-        if best is None:
-            tuned_now = True
-            timings = []
-            last_exc = None
-            for cfg in self.configs:
-                call_kwargs = {**kwargs, **cfg.kwargs, "num_warps": cfg.num_warps,
-                               "num_stages": cfg.num_stages}
+        result = Tuning()
+        for cfg in self.configs:
+            def one_run(cfg=cfg):
+                binding.zero(self.reset_to_zero)
+                self._launch_with(grid, args, kwargs, cfg)
+            try:
+                result.ranked.append((do_bench(one_run, warmup=self.warmup, rep=self.rep), cfg))
+            except Exception as exc:  # this Config cannot run here
+                result.failed.append((cfg, exc))
+        result.ranked.sort(key=lambda entry: entry[0])
+        return result
 
-                def run_cfg(call_kwargs=call_kwargs):
-                    for name in self.reset_to_zero:
-                        bound[name].zero_()
-                    self.jitfn[grid](*args, **call_kwargs)
-
-                try:
-                    ms = do_bench(run_cfg, warmup=self.warmup, rep=self.rep)
-                    timings.append((ms, cfg))
-                except Exception as e:  # invalid config (LDS, tiling, ...)
-                    last_exc = e
-                    continue
-            if not timings:
-                raise RuntimeError(f"autotune: no valid config for {self.__name__}") from last_exc
-            timings.sort(key=lambda t: t[0])
-            self.timings[keyv] = timings
-            best = timings[0][1]
-            self.cache[keyv] = best
-        self.best_config = best
-        if tuned_now:
-            for name in self.reset_to_zero:
-                bound[name].zero_()
-        self.jitfn[grid](*args, **{**kwargs, **best.kwargs, "num_warps": best.num_warps,
-                                   "num_stages": best.num_stages})
+    def _launch(self, grid, *args, **kwargs):
+        binding = _Binding(self.jitfn, args, kwargs)
+        key = binding.tuning_key(self.key)
+        cfg = self.cache.get(key)
+        if cfg is None:
+            tuning = self.tune(grid, args, kwargs, binding)
+            self.failures[key] = tuning.failed
+            if not tuning.ranked:
+                last = tuning.failed[-1][1] if tuning.failed else None
+                raise RuntimeError(f"autotune: no valid config for {self.__name__}") from last
+            self.timings[key] = tuning.ranked
+            cfg = self.cache[key] = tuning.best
+            binding.zero(self.reset_to_zero)     # undo the timed runs' writes
+        self.best_config = cfg
+        return self._launch_with(grid, args, kwargs, cfg)
 
 
 def autotune(configs, key, reset_to_zero=None):
-    def deco(jitfn):
-        return Autotuner(jitfn, configs, key, reset_to_zero)
-
-    return deco
+    """@newt.autotune(configs, key, reset_to_zero=None) over a @newt.jit kernel."""
+    return lambda jitfn: Autotuner(jitfn, configs, key, reset_to_zero)
 
 
 class Heuristics:
+    """A JIT function whose named constexprs are computed from each call's
+    arguments: `values` maps a constexpr name to fn(arguments by name)."""
+
     def __init__(self, jitfn, values):
         self.jitfn = jitfn
-        self.values = values
+        self.values = dict(values)
         self.__name__ = getattr(jitfn, "__name__", "kernel")
         self.param_names = jitfn.param_names
         self.defaults = getattr(jitfn, "defaults", {})
 
     def __getitem__(self, grid):
-        def runner(*args, **kwargs):
-            bound = dict(zip(self.jitfn.param_names, args))
-            bound.update(kwargs)
-            for name, fn in self.values.items():
-                kwargs[name] = fn(bound)
-            return self.jitfn[grid](*args, **kwargs)
-
-        return runner
+        def launch(*args, **kwargs):
+            named = _Binding(self.jitfn, args, kwargs).values
+            derived = {name: rule(named) for name, rule in self.values.items()}
+            return self.jitfn[grid](*args, **{**kwargs, **derived})
+        return launch
 
 
 def heuristics(values):
-    def deco(jitfn):
-        return Heuristics(jitfn, values)
-
-    return deco
+    """@newt.heuristics({name: fn(args)}) over a @newt.jit (or autotuned) kernel."""
+    return lambda jitfn: Heuristics(jitfn, values)

@@ -3,6 +3,8 @@
 These are user-level kernels exactly as a newt user writes them (the
 reference's examples/01-05), extended to the benchmark configurations:
   add_kernel        examples/01_vector_add.py:14-21 (unchanged)
+  copy_kernel       no reference counterpart: a streaming copy that measures
+                    the HBM ceiling of a kernel compiled by newt (bench.py)
   softmax_kernel    examples/02_fused_softmax.py:15-24 (unchanged)
   layernorm_kernel  examples/03_layernorm.py:13-27 + stores of the saved
                     per-row mean / rstd (config 3 asks for them)
@@ -17,6 +19,11 @@ reference's examples/01-05), extended to the benchmark configurations:
                     instructions per element); launched with waves_per_eu=2 so
                     two waves share each SIMD and one wave's softmax runs while
                     the other's MFMAs do
+  attention_plain_kernel
+                    examples/05_fused_attention.py:14-48 as written there
+                    (nl.exp, qk * scale, a where mask), generalised only by the
+                    batch*head axis and the causal mask; also the kernel for a
+                    scale <= 0
   dt_matmul         examples/deuteron/01_matmul.py (unchanged body): the tile
                     DSL traced to newt and autotuned against its eager oracle
 Everything is compiled by newt_amd's compiler to HIP for gfx950.
@@ -46,6 +53,21 @@ def add(x, y, out=None, BLOCK=1024, num_warps=4):
     n = x.numel()
     add_kernel[(newt.cdiv(n, BLOCK),)](x, y, out, n, BLOCK=BLOCK, num_warps=num_warps)
     return out
+
+
+@newt.jit
+def copy_kernel(src_ptr, dst_ptr, n, BLOCK: nl.constexpr):
+    # a one-read-one-write stream: the HBM ceiling any kernel compiled by
+    # newt that reads and writes its bytes once can reach at a given size
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    mask = offs < n
+    nl.store(dst_ptr + offs, nl.load(src_ptr + offs, mask=mask), mask=mask)
+
+
+def copy(src, dst, BLOCK=4096, num_warps=4):
+    n = src.numel()
+    copy_kernel[(newt.cdiv(n, BLOCK),)](src, dst, n, BLOCK=BLOCK, num_warps=num_warps)
+    return dst
 
 
 # ---------------------------------------------------------------------------
@@ -269,12 +291,84 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
              mask=qmask)
 
 
+@newt.jit
+def attention_plain_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
+                           sqb, sqh, sqm, skb, skh, skn, svb, svh, svn, sob, soh, som,
+                           BLOCK_M: nl.constexpr, BLOCK_N: nl.constexpr, D: nl.constexpr,
+                           CAUSAL: nl.constexpr):
+    # examples/05_fused_attention.py:14-48 as written there (one key loop,
+    # nl.exp, qk * scale, a where mask, p cast to V's dtype), generalised only
+    # by the batch*head grid axis and the causal mask with its loop bound
+    pid = nl.program_id(0)
+    bh = nl.program_id(1)
+    bi = bh // H
+    hi = bh % H
+    q_base = q_ptr + bi * sqb + hi * sqh
+    k_base = k_ptr + bi * skb + hi * skh
+    v_base = v_ptr + bi * svb + hi * svh
+    o_base = o_ptr + bi * sob + hi * soh
+    offs_m = pid * BLOCK_M + nl.arange(0, BLOCK_M)
+    offs_d = nl.arange(0, D)
+    qmask = offs_m[:, None] < S
+    q = nl.load(q_base + offs_m[:, None] * sqm + offs_d[None, :], mask=qmask, other=0.0)
+
+    m_i = nl.full((BLOCK_M,), float("-inf"), dtype=nl.float32)
+    l_i = nl.zeros((BLOCK_M,), dtype=nl.float32)
+    acc = nl.zeros((BLOCK_M, D), dtype=nl.float32)
+
+    end_n = S
+    if CAUSAL:
+        end_n = nl.minimum(S, (pid + 1) * BLOCK_M)
+    for start_n in range(0, end_n, BLOCK_N):
+        offs_n = start_n + nl.arange(0, BLOCK_N)
+        nmask = offs_n[:, None] < S
+        k = nl.load(k_base + offs_n[:, None] * skn + offs_d[None, :], mask=nmask, other=0.0)
+        qk = nl.dot(q, nl.trans(k)) * scale
+        if CAUSAL:
+            qk = nl.where((offs_n[None, :] < S) & (offs_m[:, None] >= offs_n[None, :]),
+                          qk, float("-inf"))
+        else:
+            qk = nl.where(offs_n[None, :] < S, qk, float("-inf"))
+        m_new = nl.maximum(m_i, nl.max(qk, axis=1))
+        alpha = nl.exp(m_i - m_new)
+        p = nl.exp(qk - m_new[:, None])
+        l_i = l_i * alpha + nl.sum(p, axis=1)
+        acc = acc * alpha[:, None]
+        v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :], mask=nmask, other=0.0)
+        acc = nl.dot(p.to(v_ptr.dtype.element_ty), v, acc)
+        m_i = m_new
+
+    acc = acc / l_i[:, None]
+    nl.store(o_base + offs_m[:, None] * som + offs_d[None, :], acc, mask=qmask)
+
+
 def attention(q, k, v, causal=False, scale=None, out=None, BLOCK_M=128, BLOCK_N=64,
-              num_warps=4, num_stages=2, waves_per_eu=2):
+              num_warps=4, num_stages=2, waves_per_eu=2, plain=False):
+    """Flash attention forward over [B, H, S, D] tensors (unit stride along D).
+
+    plain=True launches attention_plain_kernel (the examples/05 form). A
+    scale <= 0 always does: the default kernel folds the scale into the
+    exponent and takes max(qk) * scale as the row maximum, which holds only
+    for a positive scale."""
     B, H, S, D = q.shape
+    for t in (q, k, v):
+        if t.stride(3) != 1:
+            raise ValueError("attention: q, k and v need unit stride along head_dim")
     out = torch.empty_like(q) if out is None else out
-    scale = D ** -0.5 if scale is None else scale
+    if out.stride(3) != 1:
+        raise ValueError("attention: out needs unit stride along head_dim")
+    scale = D ** -0.5 if scale is None else float(scale)
     grid = (newt.cdiv(S, BLOCK_M), B * H)
+    if plain or not scale > 0:
+        attention_plain_kernel[grid](q, k, v, out, S, H, scale,
+                                     q.stride(0), q.stride(1), q.stride(2),
+                                     k.stride(0), k.stride(1), k.stride(2),
+                                     v.stride(0), v.stride(1), v.stride(2),
+                                     out.stride(0), out.stride(1), out.stride(2),
+                                     BLOCK_M=BLOCK_M, BLOCK_N=BLOCK_N, D=D, CAUSAL=causal,
+                                     num_warps=num_warps, num_stages=num_stages,
+                                     waves_per_eu=waves_per_eu)
+        return out
     attention_kernel[grid](q, k, v, out, S, H, scale,
                            q.stride(0), q.stride(1), q.stride(2),
                            k.stride(0), k.stride(1), k.stride(2),

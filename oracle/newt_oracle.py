@@ -91,27 +91,31 @@ def matmul(a, b, out_dtype="float32"):
     return round_to((a @ b).astype(np.float32), out_dtype)
 
 
-def attention(q, k, v, scale, causal=False, p_dtype=None, out_dtype="float32"):
+def attention(q, k, v, scale, causal=False, p_dtype=None, out_dtype="float32",
+              q_pos=None):
     """examples/05_fused_attention.py:14-48 generalised to [B, H, S, D]:
     S = q k^T * scale, optional causal mask (key index <= query index),
     P = softmax(S) (fp32 state), P rounded to the value dtype before P @ V
     (the reference casts p to the MMA dtype), O = P V / rowsum.
     The normalisation uses the unrounded row sums, as the online-softmax
-    kernel accumulates l_i from the fp32 probabilities."""
+    kernel accumulates l_i from the fp32 probabilities.
+    q_pos: sequence positions of q's rows when q holds a subset of them
+    (default 0..M-1); the causal mask compares key indices with these."""
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
-    s = np.einsum("...md,...nd->...mn", q, k) * scale
+    s = (q @ np.swapaxes(k, -1, -2)) * scale
     if causal:
         M, N = s.shape[-2:]
-        keep = np.arange(N)[None, :] <= np.arange(M)[:, None]
+        pos = np.arange(M) if q_pos is None else np.asarray(q_pos)
+        keep = np.arange(N)[None, :] <= pos[:, None]
         s = np.where(keep, s, -np.inf)
     m = s.max(axis=-1, keepdims=True)
     p = np.exp(s - m)
     l = p.sum(axis=-1, keepdims=True)
     if p_dtype is not None:
         p = round_to(p.astype(np.float32), p_dtype).astype(np.float64)
-    o = np.einsum("...mn,...nd->...md", p, v) / l
+    o = (p @ v) / l
     return round_to(o.astype(np.float32), out_dtype)
 
 
@@ -119,6 +123,37 @@ def rel_frobenius(actual, expected):
     a = np.asarray(actual, np.float64)
     e = np.asarray(expected, np.float64)
     return float(np.linalg.norm(a - e) / max(np.linalg.norm(e), 1e-30))
+
+
+# relative spacing of a value's binade: ulp(x) <= REL_ULP * |x| for normal x
+REL_ULP = {"float16": 2.0 ** -10, "bfloat16": 2.0 ** -7, "float32": 2.0 ** -23}
+
+
+def ulp_violations(actual, expected, dtype, atol=1e-6):
+    """Number of elements of `actual` farther than one ulp of `dtype` (plus
+    atol, for subnormal results) from `expected`, the exact product rounded
+    to dtype. A kernel that accumulates in fp32 and rounds once lands within
+    one ulp of it; a wrong element (a wrong tile, row or column) does not."""
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    bad = np.abs(a - e) > REL_ULP[dtype] * np.abs(e) + atol
+    return int(np.count_nonzero(bad | np.isnan(a)))
+
+
+def panel_rows(M, block=64, extra=(0,)):
+    """Row indices touching every `block`-row panel of an M-row output (one
+    row per panel at an offset that cycles through the panel, so different
+    waves and lanes are sampled), plus M - 1 and `extra`."""
+    rows = {p * block + (p * 29 + 7) % block for p in range((M + block - 1) // block)}
+    rows = {r for r in rows if r < M} | {M - 1} | {r for r in extra if 0 <= r < M}
+    return np.array(sorted(rows))
+
+
+def spread(n, count):
+    """`count` indices spread over range(n), always holding 0 and n - 1."""
+    if count >= n:
+        return np.arange(n)
+    return np.unique(np.round(np.linspace(0, n - 1, count)).astype(np.int64))
 
 
 # -- brute-force forms for tiny inputs (pinning helpers) -------------------------

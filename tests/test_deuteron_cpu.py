@@ -52,45 +52,99 @@ def add_relu(x, y, out):
 def test_matmul_source_is_a_pipelineable_dot_loop():
     x, y, o = torch.empty(64, 32).half(), torch.empty(32, 48).half(), torch.empty(64, 48).half()
     src = matmul.to_newt_source(x, y, o)
-    assert "@newt.jit" in src and "def matmul_newt(" in src
+    assert "@newt.jit" in src and "def matmul__tiles(" in src
     assert "BLOCK_TILE_M: nl.constexpr" in src and "BLOCK_TILE_K: nl.constexpr" in src
     assert "nl.program_id(0)" in src and "nl.program_id(1)" in src
-    assert "for _i_tile_k in range(0, nl.cdiv(x_d1, BLOCK_TILE_K)):" in src
-    assert "acc = nl.dot(_ld1, _ld2, acc)" in src
+    assert "for tile_k_step in range(nl.cdiv(x_d1, BLOCK_TILE_K)):" in src
+    # each tensor read is its own statement; the dot consumes them directly
+    assert "v_acc = nl.dot(_t1, _t2, v_acc)" in src
     assert src.count("nl.load(") == 2 and "nl.store(" in src
-    ks = matmul._source_for((x, y, o))
-    assert ks.tunable == ["BLOCK_TILE_M", "BLOCK_TILE_N", "BLOCK_TILE_K"]
-    assert ks.store_params == {"out"}
+    assert "tile_m_in[:, None] & tile_k_in[None, :]" in src
+    tr = matmul._specialize((x, y, o)).traced
+    assert tr.tunable == ["BLOCK_TILE_M", "BLOCK_TILE_N", "BLOCK_TILE_K"]
+    assert tr.writes == {"out"} and tr.has_dot and tr.spans == []
 
 
-def test_dot_kernels_try_gfx950_priors_first():
+def test_dot_kernels_try_gfx950_seeds_first():
+    from newt_amd.deuteron.runtime import SearchSpace
     x, y, o = torch.empty(64, 32).half(), torch.empty(32, 48).half(), torch.empty(64, 48).half()
-    ks = matmul._source_for((x, y, o))
-    pri = matmul._priors(ks, matmul._space(ks))
-    assert dict(pri[0]) == {"num_warps": 4, "num_stages": 4, "BLOCK_TILE_M": 256,
-                            "BLOCK_TILE_N": 256, "BLOCK_TILE_K": 32}
-    xs, os_ = torch.empty(8, 100), torch.empty(8, 100)
-    ks2 = softmax._source_for((xs, os_))
-    assert softmax._priors(ks2, softmax._space(ks2)) == []
+    space = SearchSpace(matmul._specialize((x, y, o)).traced)
+    assert dict(space.seeds()[0]) == {"num_warps": 4, "num_stages": 4, "BLOCK_TILE_M": 256,
+                                      "BLOCK_TILE_N": 256, "BLOCK_TILE_K": 32}
+    assert all(space.admits(c) for c in space.moves(space.seeds()[0]))
+    xs = torch.empty(8, 100)
+    sm = SearchSpace(softmax._specialize((xs, xs)).traced, span_elements=128)
+    assert sm.seeds() == []
+    # footprints beyond one workgroup's registers are not tried
+    assert all(c["BLOCK_TILE_M"] * 128 <= 1 << 15 for c in sm.every())
+    assert sm.admits(sm.default())
 
 
 def test_masks_reach_reductions():
     x = torch.empty(10, 30)
     src = softmax.to_newt_source(x, x)
-    # padded lanes of the masked row load get -inf for max and 0 for sum
-    assert "float('-inf')), axis=1)" in src and "0.0), axis=1)" in src
-    assert "BLOCK_FULL0: nl.constexpr" in src
+    # padded lanes of the whole-row load become -inf for max and 0 for sum:
+    # only the folded axis is masked
+    assert "nl.max(nl.where(x_all1_in[None, :], v_row, float('-inf')), axis=1)" in src
+    assert "nl.sum(nl.where(x_all1_in[None, :], v_e, 0.0), axis=1)" in src
+    assert "SPAN_X_1: nl.constexpr" in src
 
 
-def test_scalars_and_1d_tensors():
+def test_whole_dims_meeting_share_one_span():
     x = torch.empty(10, 30)
-    src = layernorm.to_newt_source(x, x[0], x[0], x, 1e-5)
-    assert "eps" in src.split("def layernorm_newt(")[1].split(")")[0]
-    assert "w_ptr + offs_full1 * w_s0" in src
+    tr = layernorm._specialize((x, x[0], x[0], x, 1e-5)).traced
+    assert "eps" in tr.source.split("def layernorm__tiles(")[1].split(")")[0]
+    assert "w_ptr + x_all1_idx * w_s0" in tr.source
+    assert tr.spans == [("SPAN_X_1", ["x_d1", "w_d0", "b_d0", "out_d1"])]
 
 
-def _compile(ks, types, constexprs, num_warps=4, num_stages=2):
-    tree = ast.parse(ks.source)
+def test_span_sizes_must_agree():
+    from newt_amd.deuteron.runtime import _Specialization
+    x, w = torch.empty(10, 30), torch.empty(31)
+    spec = layernorm._specialize((x, w, w, x, 1e-5))
+    with pytest.raises(ValueError, match="meet in one expression"):
+        spec.span_sizes(spec.extents((x, w, w, x, 1e-5)))
+    ok = spec.span_sizes(spec.extents((x, x[0], x[0], x, 1e-5)))
+    assert ok == {"SPAN_X_1": 32}
+
+
+@dt.kernel
+def row_mean(x, out):
+    for t in dt.tile(x.shape[0]):
+        out[t] = x[t, :].mean(1)
+
+
+def test_mean_divides_by_the_true_extent():
+    x, o = torch.empty(10, 30), torch.empty(10)
+    src = row_mean.to_newt_source(x, o)
+    assert "(nl.sum(nl.where(x_all1_in[None, :], _t1, 0.0), axis=1) / (x_d1))" in src
+
+
+def test_dot_masks_an_operand_when_neither_is_zero_padded():
+    @dt.kernel
+    def expdot(x, y, out):
+        for tm, tn in dt.tile([x.shape[0], y.shape[1]]):
+            acc = dt.zeros([tm, tn], dtype=dt.float32)
+            for tk in dt.tile(x.shape[1]):
+                acc += dt.exp(x[tm, tk]) @ dt.exp(y[tk, tn])
+            out[tm, tn] = acc
+
+    @dt.kernel
+    def halfexp(x, y, out):
+        for tm, tn in dt.tile([x.shape[0], y.shape[1]]):
+            acc = dt.zeros([tm, tn], dtype=dt.float32)
+            for tk in dt.tile(x.shape[1]):
+                acc += dt.exp(x[tm, tk]) @ y[tk, tn]
+            out[tm, tn] = acc
+    x, y, o = torch.empty(64, 32), torch.empty(32, 48), torch.empty(64, 48)
+    src = expdot.to_newt_source(x, y, o)
+    assert "nl.where(tk_in[None, :], nl.exp(_t1), 0.0)" in src
+    # one raw load (zero in its padded lanes) is enough
+    assert "nl.where(" not in halfexp.to_newt_source(x, y, o)
+
+
+def _compile(tr, types, constexprs, num_warps=4, num_stages=2):
+    tree = ast.parse(tr.source)
     fndef = next(n for n in tree.body if isinstance(n, ast.FunctionDef))
     import newt
     import newt.language as nl
@@ -107,9 +161,9 @@ def _compile(ks, types, constexprs, num_warps=4, num_stages=2):
 def test_generated_matmul_compiles_pipelined_for_gfx950():
     from newt_amd.runtime import hip
     x, y, o = torch.empty(64, 32).half(), torch.empty(32, 48).half(), torch.empty(64, 48).half()
-    ks = matmul._source_for((x, y, o))
+    tr = matmul._specialize((x, y, o)).traced
     f16p = tp.pointer_type(tp.float16)
-    src, lds = _compile(ks, lambda n: f16p if n.endswith("_ptr") else tp.int32,
+    src, lds = _compile(tr, lambda n: f16p if n.endswith("_ptr") else tp.int32,
                         {"BLOCK_TILE_M": 128, "BLOCK_TILE_N": 128, "BLOCK_TILE_K": 32},
                         num_warps=4, num_stages=3)
     assert "newt::lds_dma16" in src and "_ldsP2" in src     # 3 direct-to-LDS stages
@@ -119,20 +173,24 @@ def test_generated_matmul_compiles_pipelined_for_gfx950():
 def test_generated_softmax_compiles_for_gfx950():
     from newt_amd.runtime import hip
     x = torch.empty(10, 30)
-    ks = softmax._source_for((x, x))
+    tr = softmax._specialize((x, x)).traced
     f32p = tp.pointer_type(tp.float32)
-    src, _ = _compile(ks, lambda n: f32p if n.endswith("_ptr") else tp.int32,
-                      {"BLOCK_TILE_M": 2, "BLOCK_FULL0": 32, "BLOCK_FULL1": 32})
+    src, _ = _compile(tr, lambda n: f32p if n.endswith("_ptr") else tp.int32,
+                      {"BLOCK_TILE_M": 2, "SPAN_X_1": 32})
     assert len(hip.compile_hip(src, "k")) > 0
 
 
 @pytest.mark.parametrize("body,msg", [
     ("x[0] = 1.0", "top level"),
-    ("for t in range(4):\n        pass", "expected dt.tile"),
+    ("for t in range(4):\n        pass", "dt.tile"),
     ("for t in dt.tile(x.shape[0]):\n        out[t] = x[t].to(dt.float16)", ".to()"),
-    ("for t in dt.tile(x.shape[0]):\n        out[t] = x[t].mean()", "mean"),
-    ("for t in dt.tile(x.shape[0]):\n        out[t] = q[t]", "unknown name"),
+    ("for t in dt.tile(x.shape[0]):\n        out[t] = x[t].mean()", "whole dimensions"),
+    ("for t in dt.tile(x.shape[0]):\n        out[t] = q[t]", "not defined"),
     ("for t in dt.tile(x.shape[0]):\n        out[t, t] = x[t]", "dims"),
+    ("for t in dt.tile(x.shape[0]):\n        out[t] = x[t]\n    for u in dt.tile(4):\n"
+     "        out[u] = x[u]", "exactly one"),
+    ("for t in dt.tile(x.shape[0]):\n        for u in dt.tile(x.shape[0]):\n"
+     "            out[t] = x[u] + x[t]", "cannot be combined"),
 ])
 def test_trace_errors(tmp_path, body, msg):
     import importlib.util
@@ -144,3 +202,35 @@ def test_trace_errors(tmp_path, body, msg):
     kern = dt.kernel(mod.k)
     with pytest.raises(dt.TraceError, match=msg):
         kern.to_newt_source(torch.empty(8), torch.empty(8))
+
+
+def test_config_store_merges_and_replaces_atomically(tmp_path, monkeypatch):
+    """configs.json: entries from several writers survive, a corrupt or
+    truncated file is read as empty (and then rewritten whole), and no
+    temporary file is left behind."""
+    import json
+    from newt_amd.deuteron.runtime import Config, ConfigStore
+    monkeypatch.setenv("DEUTERON_CACHE_DIR", str(tmp_path))
+    a, b = ConfigStore(), ConfigStore()
+    a.put("k1", Config(BLOCK_T=64, num_warps=4))
+    b.put("k2", Config(BLOCK_T=128, num_warps=8))
+    data = json.loads((tmp_path / "configs.json").read_text())
+    assert data == {"k1": {"BLOCK_T": 64, "num_warps": 4},
+                    "k2": {"BLOCK_T": 128, "num_warps": 8}}
+    assert a.get("k2") == {"BLOCK_T": 128, "num_warps": 8} and a.get("k3") is None
+    (tmp_path / "configs.json").write_text('{"k1": {"BLOCK_T": 6')     # truncated
+    assert a.get("k1") is None
+    a.put("k3", Config(BLOCK_T=32))
+    assert json.loads((tmp_path / "configs.json").read_text()) == {"k3": {"BLOCK_T": 32}}
+    assert sorted(p.name for p in tmp_path.iterdir()) == ["configs.json", "configs.json.lock"]
+
+
+def test_untuned_kernel_uses_a_default_and_persists_nothing(tmp_path, monkeypatch):
+    from newt_amd.deuteron.runtime import SearchSpace
+    monkeypatch.setenv("DEUTERON_CACHE_DIR", str(tmp_path))
+    k = dt.kernel(autotune=False)(matmul.fn)
+    x, y, o = torch.empty(64, 32).half(), torch.empty(32, 48).half(), torch.empty(64, 48).half()
+    spec = k._specialize((x, y, o))
+    cfg = SearchSpace(spec.traced).default()
+    assert cfg["BLOCK_TILE_M"] == 256 and cfg.num_stages == 4
+    assert not (tmp_path / "configs.json").exists()

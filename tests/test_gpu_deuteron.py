@@ -165,3 +165,39 @@ def test_config_cache_persists(tmp_path, monkeypatch):
     k2 = dt.kernel(add_relu.fn)
     k2(x, x, out)          # served from the disk cache, no autotuning
     assert dict(k2.best_config) == next(iter(data.values()))
+
+
+@dt.kernel(samples=4)
+def row_mean(x, out):
+    for t in dt.tile(x.shape[0]):
+        out[t] = x[t, :].mean(1)
+
+
+def test_mean_over_a_ragged_whole_dimension():
+    """mean() folds a whole dimension: padded lanes are excluded and the sum
+    is divided by the true extent (777, not the 1024-wide span)."""
+    x = torch.randn(300, 777, device="cuda", generator=_g(17))
+    out = torch.empty(300, device="cuda")
+    row_mean(x, out)
+    torch.testing.assert_close(out, x.mean(1), rtol=1e-5, atol=1e-6)
+
+
+@dt.kernel(config={"BLOCK_TM": 64, "BLOCK_TN": 64, "BLOCK_TK": 32, "num_warps": 4,
+                   "num_stages": 2})
+def exp_dot(x, y, out):
+    for tm, tn in dt.tile([x.shape[0], y.shape[1]]):
+        acc = dt.zeros([tm, tn], dtype=dt.float32)
+        for tk in dt.tile(x.shape[1]):
+            acc += dt.exp(x[tm, tk]) @ dt.exp(y[tk, tn])
+        out[tm, tn] = acc
+
+
+def test_dot_of_computed_tiles_over_a_ragged_k():
+    """exp(0) = 1 in both operands' padded k lanes: the tracer zeroes one
+    operand there, so K = 100 (not a multiple of 32) matches torch."""
+    x = torch.randn(128, 100, device="cuda", generator=_g(18)) * 0.1
+    y = torch.randn(100, 96, device="cuda", generator=_g(19)) * 0.1
+    out = torch.empty(128, 96, device="cuda")
+    exp_dot(x, y, out)
+    ref = x.exp().double() @ y.exp().double()
+    assert ((out.double() - ref).norm() / ref.norm()).item() < 1e-5

@@ -242,3 +242,39 @@ def test_attention_golden(W):
         t = lambda k: torch.from_numpy(g[k]).bfloat16().cuda()
         o = W.attention(t("q"), t("k"), t("v"), causal=causal, BLOCK_M=64, BLOCK_N=64)
         assert orc.rel_frobenius(npf(o), g["out"]) <= 1e-2
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,H,S,D,BM,BN", [(1, 2, 256, 128, 128, 64), (2, 2, 300, 128, 128, 64),
+                                           (1, 2, 200, 64, 64, 64), (1, 1, 1000, 128, 128, 64)])
+def test_attention_plain_form(W, causal, B, H, S, D, BM, BN):
+    """The examples/05 form (nl.exp, qk * scale, a where mask in one loop)
+    compiled as written, ragged sequence lengths included."""
+    q, k, v = (seeded((B, H, S, D), s, dtype=torch.bfloat16) for s in (26, 27, 28))
+    o = W.attention(q, k, v, causal=causal, plain=True, BLOCK_M=BM, BLOCK_N=BN)
+    ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    assert orc.rel_frobenius(npf(o), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [-0.1, 0.0, -1.0])
+def test_attention_non_positive_scale(W, causal, scale):
+    """Any softmax scale is valid, as in the reference (qk * scale, then the
+    -inf mask): a scale <= 0 must not turn masked scores into +inf or NaN."""
+    B, H, S, D = 1, 2, 300, 128
+    q, k, v = (seeded((B, H, S, D), s, dtype=torch.bfloat16) for s in (36, 37, 38))
+    o = W.attention(q, k, v, causal=causal, scale=scale)
+    assert torch.isfinite(o).all()
+    ref = orc.attention(npf(q), npf(k), npf(v), scale, causal, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    assert orc.rel_frobenius(npf(o), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("n", [1, 4095, 4096 * 3 + 17, 1 << 22])
+def test_copy_exact(W, n):
+    """The streaming copy bench.py times as the HBM ceiling moves every bit."""
+    src = seeded(n, 40)
+    dst = torch.full_like(src, float("nan"))
+    W.copy(src, dst)
+    assert torch.equal(dst, src)

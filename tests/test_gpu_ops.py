@@ -1,10 +1,11 @@
 """Every nl.* operation on the GPU against torch, at the reference's tolerances.
 
 Semantics pinned here follow the reference's op suite (tests/test_ops.py):
-  elementwise binary ops in fp32 (rtol 1e-5) and fp16 (2e-3)       :21-68
+  elementwise binary ops in fp32, fp16 and bf16: bit-exact, with
+  signed zeros, infinities, NaN and subnormals (ref: rtol 1e-5 / 2e-3) :21-68
   int32 bit ops, shifts, C-truncating % and // (exact)             :71-117
   unary math (rtol/atol 1e-5)                                      :120-178
-  casts (float within 1e-3, int exact)                             :181-210
+  casts: bit-exact, with specials (ref: float within 1e-3)         :181-210
   axis and full reductions, fp16 sums accumulating in fp32         :213-289
   broadcast / broadcast_to / reshape / trans (exact)               :292-337
   strided, gathered and scalar loads (exact)                       :340-391
@@ -14,6 +15,7 @@ The kernels are launched through the HIP backend (hipRTC code objects,
 libnewt_hip.so); torch on the same device is the oracle.
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -73,15 +75,70 @@ TORCH_BINARY = {
 }
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def with_specials(x, dtype, seed):
+    """x with a prefix of IEEE special values: signed zeros, infinities, NaN,
+    subnormals of `dtype`, its largest finite values and values one rounding
+    step apart, in every pairing the two operand seeds produce."""
+    tiny = torch.finfo(dtype).tiny
+    big = torch.finfo(dtype).max
+    sp = torch.tensor([0.0, -0.0, float("inf"), float("-inf"), float("nan"), tiny / 4,
+                       -tiny / 2, tiny, big, -big, 1.0, -1.0, 3.0, 1e-3])
+    g = torch.Generator().manual_seed(seed)
+    pre = sp[torch.randint(0, len(sp), (512,), generator=g)].to(dtype).to("cuda")
+    return torch.cat([pre, x[512:]])
+
+
+def bits(t):
+    return t.view(torch.int16 if t.element_size() == 2 else torch.int32)
+
+
+def assert_same_bits(got, want, op=""):
+    """Bit-identical results, with NaN equal to any NaN (payloads are not
+    part of the semantics) and, for max/min, +0 equal to -0 (IEEE
+    maxNum/minNum leave the sign of a zero result unspecified)."""
+    g, w = got.cpu(), want.cpu()
+    same = bits(g) == bits(w)
+    same |= g.isnan() & w.isnan()
+    if op in ("maximum", "minimum"):
+        same |= (g == 0) & (w == 0)
+    bad = (~same).nonzero().flatten()
+    assert bad.numel() == 0, (f"{op}: {bad.numel()} elements differ, first at {bad[:5].tolist()}: "
+                              f"got {g[bad[:5]].tolist()} want {w[bad[:5]].tolist()}")
+
+
+def binary_oracle(op, a, b):
+    """The reference's elementwise semantics (codegen.py:1196-1284, :2114-2118)
+    on the CPU: fp16 operands computed in fp32 and rounded once, maximum /
+    minimum as C fmaxf / fminf (a NaN operand yields the other operand)."""
+    af, bf = a.cpu().float(), b.cpu().float()
+    if op == "maximum":
+        r = torch.from_numpy(np.fmax(af.numpy(), bf.numpy()))
+    elif op == "minimum":
+        r = torch.from_numpy(np.fmin(af.numpy(), bf.numpy()))
+    else:
+        r = TORCH_BINARY[op](af, bf)
+    return r.to(a.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("op", sorted(TORCH_BINARY))
 def test_binary(op, dtype):
+    """Elementwise binary ops are bit-exact (north_star): no contraction, IEEE
+    division, one rounding of the fp32 result for fp16/bf16, including signed
+    zeros, infinities, NaN and subnormal operands. nl.fma is fused (one
+    rounding of a*b+a) where torch's a*b+a rounds twice, so it is held to a
+    tolerance instead."""
     n = 4321
-    a, b = rnd(n, dtype, 0), rnd(n, dtype, 1, positive=True)
+    a = with_specials(rnd(n, dtype, 0), dtype, 10)
+    b = with_specials(rnd(n, dtype, 1, positive=True), dtype, 11)
     o = torch.empty_like(a)
     binary_k[(newt.cdiv(n, 1024),)](a, b, o, n, OP=op, BLOCK=1024)
-    tol = 1e-5 if dtype == torch.float32 else 2e-3
-    torch.testing.assert_close(o.float(), TORCH_BINARY[op](a, b).float(), rtol=tol, atol=tol)
+    want = binary_oracle(op, a, b)
+    if op == "fma":
+        tol = 1e-5 if dtype == torch.float32 else 2e-3
+        torch.testing.assert_close(o[512:].float().cpu(), want[512:].float(), rtol=tol, atol=tol)
+    else:
+        assert_same_bits(o, want, op)
 
 
 @newt.jit
@@ -204,21 +261,38 @@ def cast_k(x_ptr, o_ptr, n, DT: nl.constexpr, BLOCK: nl.constexpr):
     (torch.float16, torch.float32, nl.float32),
     (torch.float32, torch.bfloat16, nl.bfloat16),
     (torch.bfloat16, torch.float32, nl.float32),
+    (torch.float16, torch.bfloat16, nl.bfloat16),
+    (torch.bfloat16, torch.float16, nl.float16),
     (torch.float32, torch.int32, nl.int32),
     (torch.int32, torch.float32, nl.float32),
     (torch.int64, torch.int32, nl.int32),
     (torch.int32, torch.int64, nl.int64),
 ])
 def test_cast(src, dst, ndt):
+    """Casts are bit-exact against torch: float narrowing rounds to nearest
+    even (overflow to inf, NaN kept, subnormal results), widening is exact,
+    float -> int truncates toward zero (in-range values: C leaves the rest
+    undefined), int -> float rounds to nearest even."""
     n = 1000
     x = (rnd(n, seed=4) * 10).to(src)
+    if src.is_floating_point:
+        x = with_specials(x, src, 12)
+        if dst.is_floating_point:
+            # values near the destination's overflow and subnormal ranges
+            x[512:520] = torch.tensor([65504.0, 65520.0, 7e4, -7e4, 6e-8, 3e-8, 1e-40, -1e-39]
+                                      ).to(src)
+        else:
+            x = torch.where(x.isfinite() & (x.abs() < 2.0 ** 31), x, torch.zeros_like(x))
+    elif src == torch.int32 and dst.is_floating_point:
+        x[:8] = torch.tensor([16777217, -16777219, 2 ** 31 - 1, -2 ** 31, 0, 1, 33554435,
+                              -100000001], dtype=src)
     o = torch.empty(n, device="cuda", dtype=dst)
     cast_k[(1,)](x, o, n, DT=ndt, BLOCK=1024)
-    want = x.to(dst)
+    want = x.cpu().to(dst)
     if dst.is_floating_point:
-        torch.testing.assert_close(o.float(), want.float(), rtol=1e-3, atol=1e-3)
+        assert_same_bits(o, want, "cast")
     else:
-        assert torch.equal(o, want)
+        assert torch.equal(o.cpu(), want)
 
 
 def test_cast_rounds_to_nearest_even():

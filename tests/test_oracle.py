@@ -228,3 +228,55 @@ def test_checks_reject_planted_mistakes():
     assert orc.rel_frobenius(full, at["out"]) > 0.1
     wrong_scale = orc.attention(at["q"], at["k"], at["v"], 1.0, causal=True)
     assert orc.rel_frobenius(wrong_scale, at["out"]) > 1e-2
+
+
+# ---------------------------------------------------------------- sampled checks
+
+def test_attention_query_subset_matches_full_rows():
+    """q_pos: a subset of query rows, masked by their own positions, gives
+    exactly those rows of the full causal result (and of the non-causal one)."""
+    at = gold("attention_1x2x64x32_causal")
+    q, k, v = at["q"], at["k"], at["v"]
+    rows = np.array([0, 5, 31, 32, 63])
+    for causal in (False, True):
+        full = orc.attention(q, k, v, 32 ** -0.5, causal)
+        sub = orc.attention(q[:, :, rows], k, v, 32 ** -0.5, causal, q_pos=rows)
+        np.testing.assert_array_equal(sub, full[:, :, rows])
+    np.testing.assert_allclose(full, at["out"], rtol=1e-5, atol=1e-6)
+    # positions ignored (0..4 assumed) would mask the wrong keys
+    wrong = orc.attention(q[:, :, rows], k, v, 32 ** -0.5, True)
+    assert orc.rel_frobenius(wrong, full[:, :, rows]) > 0.1
+
+
+def test_ulp_violations():
+    rng = np.random.default_rng(11)
+    exact = rng.standard_normal(10000) * 0.02
+    for dt, rel in (("float16", 2.0 ** -10), ("bfloat16", 2.0 ** -7)):
+        ref = orc.round_to(exact.astype(np.float32), dt)
+        assert orc.ulp_violations(ref, ref, dt) == 0
+        # one ulp away in either direction (the neighbour in the dtype) passes
+        up = ref.astype(np.float64) + np.abs(ref) * rel / 2  # half the binade step
+        assert orc.ulp_violations(up, ref, dt) == 0
+        # a wrong element, a swapped pair and a NaN are counted
+        bad = ref.copy()
+        bad[17] *= -1
+        bad[[100, 200]] = bad[[200, 100]]
+        bad[300] = np.nan
+        assert orc.ulp_violations(bad, ref, dt) >= 3
+        # three ulps off everywhere is rejected
+        assert orc.ulp_violations(ref * (1 + 3 * rel), ref, dt) > 9000
+    # fp16 subnormals: the absolute slack covers their fixed 2^-24 spacing
+    tiny = np.array([2.0 ** -24, 3 * 2.0 ** -24, 0.0])
+    assert orc.ulp_violations(tiny + 2.0 ** -24, tiny, "float16") == 0
+
+
+def test_panel_rows_cover_every_panel():
+    for M, block in ((4096, 64), (8192, 256), (1000, 64), (64, 64), (1, 64)):
+        rows = orc.panel_rows(M, block)
+        assert rows.min() >= 0 and rows.max() == M - 1
+        assert set(rows // block) == set(range((M + block - 1) // block))
+        # offsets within the panel vary (not the same wave/lane every time)
+        if M // block > 4:
+            assert len(set(rows % block)) > 4
+    s = orc.spread(128, 8)
+    assert s[0] == 0 and s[-1] == 127 and len(s) == 8
