@@ -190,6 +190,20 @@ def bracketed_launches(fn, steps):
     return total
 
 
+SETTLE_S = 0.4
+
+
+def settle_clocks(fn, seconds):
+    """Launch fn back to back, in batches timed on the GPU, until `seconds` of
+    GPU time have passed; returns what ran (launches, seconds) for the
+    report. Untimed with respect to the measurement that follows."""
+    done, spent, batch = 0, 0.0, 50
+    while spent < seconds:
+        spent += bracketed_launches(lambda: [fn() for _ in range(batch)], 1) * 1e-3
+        done += batch
+    return {"launches": done, "gpu_s": round(spent, 3)}
+
+
 def cpu_info():
     """This host's CPU model and physical core count (from /proc/cpuinfo),
     logical CPUs, the CPUs this process may run on and torch's threads."""
@@ -330,6 +344,10 @@ def main():
     # follows the timed region instead of preceding it
     for _ in range(args.warmup):
         step()
+    # and then until the clocks have settled: whatever W is, launches run back
+    # to back for SETTLE_S seconds of GPU time (measured: right after the
+    # host-side autotuning the first ~50 launches at 4096^3 run ~20% slow)
+    settle = settle_clocks(step, SETTLE_S)
     # the timed region: K back-to-back launches between one event pair (any
     # per-launch event adds ~3.5-4.5 us per step); each launch's own duration
     # then comes from a second pass of K launches whose dispatches record events
@@ -369,6 +387,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
                      "traffic": matmul_traffic(cfg)},
+        "settle": settle,
         "kernel_ms_back_to_back_median": round(statistics.median(kern_list), 5),
         "kernel_ms_flushed_median": round(statistics.median(cold), 5),
         "tflops_flushed_median": round(flop / (statistics.median(cold) * 1e-3) / 1e12, 2),
@@ -500,19 +519,13 @@ def _secondary_workloads():
     return out
 
 
-def warm_up(fn, seconds=0.03):
+def warm_up(fn, seconds=0.2):
     """Run fn back to back for about `seconds` of GPU time, so the timing that
     follows does not start on clocks that dropped while the host was busy."""
     import torch
     fn()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    fn()
-    torch.cuda.synchronize()
-    one = max(time.perf_counter() - t0, 1e-6)
-    for _ in range(min(2000, int(seconds / one))):
-        fn()
-    torch.cuda.synchronize()
+    settle_clocks(fn, seconds)
 
 
 def secondary(cpu=True, cpu_budget=2.0):
@@ -589,8 +602,7 @@ def secondary(cpu=True, cpu_budget=2.0):
             W.matmul(a, b, c)                           # autotune
             cfg = tuned.best_config
             run = lambda: W.matmul(a, b, c, config=cfg)
-            for _ in range(min(500, max(10, int(0.02 / (2.0 * S ** 3 / 1e15))))):
-                run()                                   # ~20 ms warm-up (clocks)
+            warm_up(run)
             _, kern = timed_launches(run, 20)
             v = 2.0 * S ** 3 / (kern * 1e-3) / 1e12
             dname = {torch.float16: "float16", torch.bfloat16: "bfloat16",
@@ -623,8 +635,7 @@ def secondary(cpu=True, cpu_budget=2.0):
         b = seeded((S, S), 5, scale=S ** -0.5, dtype=torch.float16)
         c = torch.empty(S, S, device="cuda", dtype=torch.float16)
         k(a, b, c)                                      # trace + autotune
-        for _ in range(150):
-            k(a, b, c)                                  # warm-up (clocks)
+        warm_up(lambda: k(a, b, c))
         _, kern = timed_launches(lambda: k(a, b, c), 20)
         v = 2.0 * S ** 3 / (kern * 1e-3) / 1e12
         err, bad = check_matmul(a, b, c, "float16")

@@ -89,26 +89,58 @@ def _arch():
     return name
 
 
-def code_object(source, name):
-    """hipRTC-compile (or fetch from the disk cache) a kernel's code object."""
+def cache_key(source):
+    """Disk-cache key of a kernel's code object: the generated HIP source,
+    the device-template header it includes, the target, the hipRTC version,
+    this backend's version and the compile options."""
     key_src = "\n".join([source, _hip.device_header(), _arch(), str(_hip.rtc_version()),
                          _hip.BACKEND_VERSION, " ".join(_hip.COMPILE_OPTIONS)])
-    key = hashlib.sha256(key_src.encode()).hexdigest()[:32]
-    path = os.path.join(_cache_dir(), f"{key}.hsaco")
-    if os.path.exists(path):
+    return hashlib.sha256(key_src.encode()).hexdigest()[:32]
+
+
+def _write_atomic(path, data):
+    tmp = f"{path}.{os.getpid()}.tmp"
+    with open(tmp, "wb") as f:
+        f.write(data)
+    os.replace(tmp, path)
+
+
+def _cached_image(path):
+    """The code object at `path` if the sha256 recorded beside it (`.sha256`)
+    matches its bytes and it is an ELF image; None when the file is missing,
+    truncated, corrupted or has no digest (the caller then recompiles)."""
+    try:
         with open(path, "rb") as f:
-            return f.read()
+            code = f.read()
+        with open(path[:-len(".hsaco")] + ".sha256") as f:
+            want = f.read().strip()
+    except OSError:
+        return None
+    if code[:4] != b"\x7fELF" or hashlib.sha256(code).hexdigest() != want:
+        return None
+    return code
+
+
+def code_object(source, name):
+    """hipRTC-compile (or fetch from the disk cache) a kernel's code object.
+
+    Cache entries under NEWT_CACHE_DIR (default ~/.newt/cache) are
+    <key>.hsaco (the image hipModuleLoadData receives), <key>.sha256 (its
+    digest, checked on the host before the image is used) and <key>.hip (the
+    source, for inspection). An entry that fails the check is rebuilt."""
+    key = cache_key(source)
+    base = os.path.join(_cache_dir(), key)
+    code = _cached_image(base + ".hsaco")
+    if code is not None:
+        return code
     try:
         code = _hip.compile_hip(source, name, _arch())
     except _hip.HIPRTCError as e:
         lined = "\n".join(f"{i + 1:4d} | {ln}" for i, ln in enumerate(source.splitlines()))
         raise _hip.HIPRTCError(f"{e}\n--- generated source ---\n{lined}") from None
-    tmp = f"{path}.{os.getpid()}.tmp"
-    with open(tmp, "wb") as f:
-        f.write(code)
-    os.replace(tmp, path)
-    with open(os.path.join(_cache_dir(), f"{key}.hip"), "w") as f:
-        f.write(source)
+    _write_atomic(base + ".hsaco", code)
+    _write_atomic(base + ".sha256", hashlib.sha256(code).hexdigest().encode())
+    _write_atomic(base + ".hip", source.encode())
     return code
 
 
