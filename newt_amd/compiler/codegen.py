@@ -56,8 +56,10 @@ _CMP = {ast.Eq: "==", ast.NotEq: "!=", ast.Lt: "<", ast.LtE: "<=", ast.Gt: ">",
 _MATH = {  # name -> (fp32 fn, fp64 fn)
     # fp32 exp2 is the hardware v_exp_f32 (1 ulp); results below 2**-126 flush
     # to zero instead of taking the library's denormal-scaling path, which
-    # would cost a compare, two selects and an ldexp per element
-    "exp": ("expf", "exp"), "exp2": ("__builtin_amdgcn_exp2f", "exp2"), "log": ("logf", "log"),
+    # would cost a compare, two selects and an ldexp per element. fp32 exp is
+    # exp2(x * log2 e) on the same unit (newt::exp_f32: relative error under
+    # 8e-6 over the whole range, within the reference's 1e-5 for exp)
+    "exp": ("newt::exp_f32", "exp"), "exp2": ("__builtin_amdgcn_exp2f", "exp2"), "log": ("logf", "log"),
     "log2": ("log2f", "log2"), "sqrt": ("sqrtf", "sqrt"), "rsqrt": ("rsqrtf", "rsqrt"),
     "sin": ("sinf", "sin"), "cos": ("cosf", "cos"), "tanh": ("tanhf", "tanh"),
     "erf": ("erff", "erf"), "floor": ("floorf", "floor"), "ceil": ("ceilf", "ceil"),
@@ -1762,7 +1764,7 @@ class Codegen(ast.NodeVisitor):
         d = self.cdtype(x)
         cd = tp.compute_dtype(d)
         one = "1.0" if cd == tp.float64 else "1.0f"
-        ex = "exp" if cd == tp.float64 else "expf"
+        ex = "exp" if cd == tp.float64 else "newt::exp_f32"
         return self.elementwise(node, [x], d, lambda es: self.conv(
             f"({one} / ({one} + {ex}(-({self.conv(es[0], d, cd)}))))", cd, d))
 
@@ -1807,6 +1809,12 @@ class Codegen(ast.NodeVisitor):
         if isinstance(cond, Const):
             return a if cond.pyval else b
         rd = tp.promote(self.cdtype(a), self.cdtype(b))
+        st = self.pipe_active
+        if st is not None and st.get("fast") and id(node) in st.get("true_wheres", ()):
+            # the branch-free copy of a pipelined loop runs only iterations in
+            # which this mask is all-true (its entry test proved it)
+            return self.elementwise(node, [cond, a, b], rd,
+                                    lambda es: self.to_compute(es[1], a, rd))
         fast = None
         if isinstance(cond, Block):
             # a mask that one uniform test proves all-true (interior tiles of a

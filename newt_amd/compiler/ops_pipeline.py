@@ -50,7 +50,7 @@ import os
 
 from . import layouts as lo
 from . import types as tp
-from .values import Affine, Const, LazyLoad, Reg, Staged
+from .values import Affine, Block, Const, LazyLoad, Reg, Scalar, Staged, Sym
 
 _SIDE_EFFECTS = {"store", "atomic_add", "atomic_max", "atomic_min"}
 
@@ -294,9 +294,34 @@ class DotPipeline:
             masks = [k.value for k in call.keywords if k.arg == "mask"] + list(call.args[1:2])
             if any(_kform(m, kinds) not in ("b", "c") for m in masks):
                 fast_ok = False
+        # where() masks of the loop body whose condition is also such a
+        # conjunction (bounds and causal masks): the branch-free copy can run
+        # only iterations where they are all-true and select without them
+        advance_idx = set(assigned[nm][0] for nm in carried)
+        staged_idx = set(rec["index"] for rec in staged.values())
+        wheres, wneed = [], set()
+        for i, st_ in enumerate(flat):
+            if i in slice_idx or i in advance_idx or i in staged_idx:
+                continue
+            for nd in ast.walk(st_):
+                if (_callee(nd) == "where" and len(nd.args) == 3 and not nd.keywords
+                        and _kform(nd.args[0], kinds) == "b"):
+                    wheres.append(nd)
+                    wneed |= _names_read(nd.args[0])
+        where_deps = set()
+        changed = True
+        while changed:
+            changed = False
+            for i, st_ in enumerate(flat):
+                nm = _target(st_)
+                if nm in konly and nm in wneed and i not in where_deps:
+                    where_deps.add(i)
+                    wneed |= _names_read(st_.value)
+                    changed = True
         return {"flat": flat, "staged": staged, "slice": sorted(slice_idx),
-                "advance": sorted(assigned[nm][0] for nm in carried), "konly": konly,
-                "kname": kname, "node": node, "fast_ok": fast_ok}
+                "advance": sorted(advance_idx), "konly": konly,
+                "kname": kname, "node": node, "fast_ok": fast_ok,
+                "wheres": wheres, "where_deps": sorted(where_deps)}
 
     # ----------------------------------------------------------- emission
     def pipelined_for(self, node, plan, lo_, hi, st, idt):
@@ -437,6 +462,8 @@ class DotPipeline:
         j < m+1 when it holds at j = 0 and at j = m. m = n-1 covers divisible
         loops, m = n-2 a ragged last tile; otherwise no iteration is fast."""
         node, state, S, n, lo_e, stv, idt, slice_stmts, advance, skip, temps, kname, flat = ctx
+        if state["plan"]["wheres"] and os.environ.get("NEWT_WHERE_VERSION", "1") != "0":
+            return self._fast_prefix(ctx)
         conds = []
         for j in ("0", f"({n.expr} - 1)", f"({n.expr} - 2)"):
             self.locals[kname] = self.new_scalar(idt, f"({lo_e} + {j} * {stv})")
@@ -446,6 +473,55 @@ class DotPipeline:
                 self.locals.pop(t, None)
         c0, c1, c2 = conds
         return self.new_scalar(idt, f"(({c0}) ? (({c1}) ? {n.expr} : (({c2}) ? ({n.expr} - 1) : 0)) : 0)")
+
+    def _fast_prefix(self, ctx):
+        """Number of leading iterations j in which every DMA tile is a whole
+        in-bounds copy and every versioned where() mask is all-true. Each
+        condition is a conjunction of comparisons affine in j, so the set of
+        iterations where all of them hold is an interval; when it holds at
+        j = 0 that interval is a prefix, whose length a binary search finds
+        (a causal mask ends it at the diagonal, not at the last iteration).
+        Records which where() masks the branch-free copy may drop."""
+        node, state, S, n, lo_e, stv, idt, slice_stmts, advance, skip, temps, kname, flat = ctx
+        plan = state["plan"]
+        in_slice = set(plan["slice"])
+        deps = [flat[i] for i in plan["where_deps"] if i not in in_slice]
+        dep_names = {_target(x) for x in deps}
+
+        def cond_at(j):
+            self.locals[kname] = self.new_scalar(idt, f"({lo_e} + ({j}) * {stv})")
+            self.visit_body(slice_stmts)
+            parts = [self.pipe_dma_condition(state)]
+            self.visit_body(deps)
+            proven = []
+            for nd in plan["wheres"]:
+                v = self.visit_expr(nd.args[0])
+                full = self.mask_all_true(v, v.shape) if isinstance(v, Block) else None
+                if full is not None and full != "false":
+                    parts.append(f"({full})")
+                    proven.append(id(nd))
+            for t in temps | dep_names:
+                self.locals.pop(t, None)
+            return " && ".join(p for p in parts if p != "true") or "true", proven
+
+        c0, proven = cond_at("0")
+        state["true_wheres"] = set(proven)
+        fm, lo, hi, mid = (self.fresh(x) for x in ("fm", "lo", "hi", "mid"))
+        self.emit(f"int {fm} = 0;")
+        self.emit(f"if ({n.expr} > 0 && ({c0})) {{")
+        self.indent += 1
+        self.emit(f"int {lo} = 1, {hi} = {n.expr};")
+        self.emit(f"while ({lo} < {hi}) {{")
+        self.indent += 1
+        self.emit(f"const int {mid} = ({lo} + {hi}) >> 1;")
+        cm, _ = cond_at(mid)
+        self.emit(f"if ({cm}) {lo} = {mid} + 1; else {hi} = {mid};")
+        self.indent -= 1
+        self.emit("}")
+        self.emit(f"{fm} = {lo};")
+        self.indent -= 1
+        self.emit("}")
+        return Scalar(idt, fm, Sym(fm, None, 1))
 
     def pipe_dma_condition(self, state):
         """Uniform condition under which every DMA tile of the slice just
