@@ -52,6 +52,21 @@ def _split_dot_axes(fndef):
     and column panel j of the other. Dependence is followed through
     assignments by name (an over-approximation: it only ever adds axes, so an
     unclear case is not matched)."""
+    _, axes = _pid_taint(fndef)
+    for n in ast.walk(fndef):
+        if _callee_name(n) == "dot" and len(n.args) >= 2:
+            a, b = axes(n.args[0]), axes(n.args[1])
+            if -1 in a or -1 in b:
+                continue
+            if ({0, 1} & a, {0, 1} & b) in (({0}, {1}), ({1}, {0})):
+                return True
+    return False
+
+
+def _pid_taint(fndef):
+    """Name -> set of program axes its value depends on (-1: an axis not
+    known at compile time), followed through assignments by name; returns
+    (taint, axes) where axes(expr) is the set for an expression."""
     taint = {}
 
     def axes(expr):
@@ -74,6 +89,11 @@ def _split_dot_axes(fndef):
                 targets, value = [n.target], n.value
             elif isinstance(n, ast.For):
                 targets, value = [n.target], n.iter
+                # a range's end bound sets how many values the target takes,
+                # not which: only its start and step carry dependence
+                if _callee_name(value) == "range" and 1 <= len(value.args) <= 3:
+                    parts = [] if len(value.args) == 1 else [value.args[0]] + list(value.args[2:])
+                    value = ast.Tuple(elts=parts, ctx=ast.Load())
             else:
                 continue
             t = axes(value)
@@ -82,12 +102,67 @@ def _split_dot_axes(fndef):
                     if isinstance(e, ast.Name) and not t <= taint.get(e.id, set()):
                         taint[e.id] = taint.get(e.id, set()) | t
                         changed = True
+    return taint, axes
+
+
+def _streamed(fndef, kinds):
+    """ids of the top-level calls named in `kinds` (nl.load / nl.store) that
+    touch data no other program touches: the address depends on every
+    program axis the kernel uses (one row per program, as in softmax or
+    layernorm), the call is not inside a loop (no re-reads) and a load's value
+    does not feed nl.dot (dot operands are shared by the programs of a row or
+    column of tiles). Their lines need not stay in the caches, so they take
+    the non-temporal hint; data shared by all programs (a layernorm's weight
+    and bias) keeps the caches to itself."""
+    taint, axes = _pid_taint(fndef)
+    used = set()
     for n in ast.walk(fndef):
-        if _callee_name(n) == "dot" and len(n.args) >= 2:
-            a, b = axes(n.args[0]), axes(n.args[1])
-            if -1 in a or -1 in b:
+        if _callee_name(n) in ("program_id", "num_programs"):
+            arg = n.args[0] if n.args else next((k.value for k in n.keywords if k.arg == "axis"), None)
+            used.add(arg.value if isinstance(arg, ast.Constant) else -1)
+    if not used or -1 in used:
+        return set()
+    dot_names = {a.id for n in ast.walk(fndef) if _callee_name(n) == "dot"
+                 for a in ast.walk(n) if isinstance(a, ast.Name)}
+    out = set()
+    for st in fndef.body:
+        if isinstance(st, (ast.For, ast.While)):
+            continue
+        for n in ast.walk(st):
+            if _callee_name(n) not in kinds or not n.args:
                 continue
-            if ({0, 1} & a, {0, 1} & b) in (({0}, {1}), ({1}, {0})):
+            if isinstance(st, ast.Assign) and any(isinstance(t, ast.Name) and t.id in dot_names
+                                                  for t in st.targets):
+                continue
+            if used <= axes(n.args[0]):
+                out.add(id(n))
+    return out
+
+
+def _shares_across_programs(fndef):
+    """False only for streaming kernels: every load outside any loop, each
+    either private to its program (the address depends on every program axis
+    the kernel uses: a row of softmax) or common to all programs (no program
+    axis: a layernorm's weights). Otherwise some data may be read by a subset
+    of the programs (a matmul's row panel, one attention head's keys and
+    values), and renumbering programs so that each XCD runs a contiguous
+    range keeps that data in one L2. Streaming kernels gain nothing from the
+    renumbering and measured 2-4% slower with it (the hardware's round-robin
+    order spreads a stream over the HBM channels better)."""
+    taint, axes = _pid_taint(fndef)
+    used = set()
+    for n in ast.walk(fndef):
+        if _callee_name(n) in ("program_id", "num_programs"):
+            arg = n.args[0] if n.args else next((k.value for k in n.keywords if k.arg == "axis"), None)
+            used.add(arg.value if isinstance(arg, ast.Constant) else -1)
+    if -1 in used:
+        return True
+    in_loops = {id(n) for st in ast.walk(fndef) if isinstance(st, (ast.For, ast.While))
+                for n in ast.walk(st)}
+    for n in ast.walk(fndef):
+        if _callee_name(n) == "load" and n.args:
+            dep = axes(n.args[0])
+            if id(n) in in_loops or -1 in dep or (dep & used and not used <= dep):
                 return True
     return False
 
@@ -175,6 +250,16 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
     hints = {}
     prefer_rows = _has_row_reduction(fndef)
     group_pids = _split_dot_axes(fndef)
+    remap_pids = _shares_across_programs(fndef)
+    # NEWT_NT_LOAD=1 / NEWT_NT_STREAM=1 read / write program-private streams
+    # with the non-temporal hint. Measured on streaming kernels of 32-256 MB:
+    # loads +2-4% under XCD-renumbered program order but 1-4% slower in the
+    # hardware order these kernels now keep; stores 10-15% slower at
+    # 128-256 MiB (19% faster at 32 MB). Both stay off by default.
+    stream_loads = (_streamed(fndef, ("load",)) if os.environ.get("NEWT_NT_LOAD", "0") == "1"
+                    else set())
+    stream_stores = (_streamed(fndef, ("store",)) if os.environ.get("NEWT_NT_STREAM", "0") == "1"
+                     else set())
     # off by default: on memory-bound kernels the registers held by early loads
     # cost more occupancy than the overlap gains (layernorm 4096x8192: 86 -> 109
     # VGPRs, 5 -> 4 waves per SIMD, 7% slower)
@@ -186,6 +271,9 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
                       num_stages=num_stages, hints=hints, waves_per_eu=waves_per_eu)
         cg.prefer_rows = prefer_rows
         cg.group_pids = group_pids
+        cg.stream_loads = stream_loads
+        cg.remap_pids = remap_pids
+        cg.stream_stores = stream_stores
         try:
             src = cg.compile()
         except _Retry:

@@ -197,6 +197,7 @@ class Codegen(ast.NodeVisitor):
         self.pipe_active = None   # pipeline state while its loop body compiles
         self.pid_remap = False
         self.group_pids = False   # set by compile_fn for matmul-shaped kernels
+        self.remap_pids = True    # compile_fn: False when no data is shared by a subset of programs
         self.params = params
         vec = 1
         for _, p in params:
@@ -1595,6 +1596,8 @@ class Codegen(ast.NodeVisitor):
         attention) is spread evenly over the XCDs instead of giving one XCD
         every eighth, heaviest block. Programs are independent, so any
         bijection keeps the language's semantics (NEWT_PID_REMAP=0: identity).
+        Kernels whose programs share no data with a subset of the others
+        (remap_pids False: streaming row kernels) keep the hardware order.
 
         In a kernel where program (i, j) reads row panel i of one dot operand
         and column panel j of the other (group_pids), each XCD's range is
@@ -1604,7 +1607,7 @@ class Codegen(ast.NodeVisitor):
         row panel, which keeps an 8192^3 fp16 matmul's operands in L2/MALL
         (NEWT_PID_GROUP=G, default 4; 0 turns grouping off)."""
         ax = self._cx(node, axis, "program_id axis")
-        if os.environ.get("NEWT_PID_REMAP", "1") == "0":
+        if os.environ.get("NEWT_PID_REMAP", "1") == "0" or not self.remap_pids:
             return self.new_scalar(tp.int32, f"(int)blockIdx.{'xyz'[ax]}")
         if not self.pid_remap:
             self.pid_remap = True

@@ -181,6 +181,8 @@ class MemoryOps:
         div = self.offset_div(L, off, cbits)
         proven = ptr.base.aligned16 and div % chunk == 0
         all_true = self.mask_all_true(mask, L.shape)
+        nt = id(ld.node) in getattr(self, "stream_loads", ())
+        rd = (lambda e: f"__builtin_nontemporal_load(&{e})") if nt else (lambda e: e)
 
         def oth(s):
             if other is None:
@@ -204,14 +206,15 @@ class MemoryOps:
                     if not proven:
                         al = f"newt::aligned({addr}, {chunk * esz})"
                         cond = f"{cond} && {al}" if cond else al
-                    vec = f"newt::load_vec<{elem.ctype}, {chunk}>({addr}, {out.var} + {g});"
+                    vec = (f"newt::load_vec{'_nt' if nt else ''}<{elem.ctype}, {chunk}>({addr}, "
+                           f"{out.var} + {g});")
                     if not cond:
                         self.emit(vec)
                     else:
                         self.emit(f"if ({cond}) {{ {vec} }} else {{")
                         self.indent += 1
                         for i in range(chunk):
-                            e = f"{base}[{o} + {i}]"
+                            e = rd(f"{base}[{o} + {i}]")
                             if masked:
                                 self.emit(f"{out.at(g + i)} = _m{i} ? {e} : {oth(g + i)};")
                             else:
@@ -221,7 +224,7 @@ class MemoryOps:
                     self.indent -= 1
                     self.emit("}")
                 else:
-                    e = f"{base}[{o}]"
+                    e = rd(f"{base}[{o}]")
                     if masked:
                         m = self.ev(mask, L, g)
                         self.emit(f"{out.at(g)} = ({m}) ? {e} : {oth(g)};")
@@ -278,6 +281,12 @@ class MemoryOps:
         if not isinstance(pointer, PtrBlock):
             self.err(node, "store() expects a pointer block")
         elem = pointer.elem
+        if (isinstance(value, Block) and value.dtype != elem and value.dtype.is_floating
+                and elem.is_floating):
+            # convert the block first, as value.to(elem) would: the same
+            # rounding, and the registers of a wide accumulator are released
+            # in one pass instead of staying live across the narrowing stores
+            value = self.cast(node, value, elem)
         shape = pointer.shape
         for v in (value, mask):
             if isinstance(v, Block):
@@ -297,10 +306,11 @@ class MemoryOps:
         off = self.prepare(off, L)
         self.flush_loads()
         self.drain_dots()
-        self.emit_store(L, pointer.base, off, value, mask, elem)
+        self.emit_store(L, pointer.base, off, value, mask, elem,
+                        stream=id(node) in getattr(self, "stream_stores", ()))
         return Const(None)
 
-    def emit_store(self, L, pbase, off, value, mask, elem):
+    def emit_store(self, L, pbase, off, value, mask, elem, stream=False):
         esz = elem.itemsize
         base = pbase.expr
         gb = self.contiguous_bits(L, off)
@@ -319,6 +329,7 @@ class MemoryOps:
         # streaming row kernels slower too, so they keep plain stores.
         acc = lo.mfma_tag_instr(L.tag)
         nt = acc is not None and acc[1] == "col" and os.environ.get("NEWT_NT_STORE", "1") != "0"
+        nt = nt or stream
 
         def val(s):
             return self.conv(self.ev(value, L, s), vd, elem)

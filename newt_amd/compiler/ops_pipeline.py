@@ -575,7 +575,10 @@ class DotPipeline:
                           f"else newt::wait_vmcnt<0>();")
             else:
                 self.emit("newt::wait_vmcnt<0>();")
-            self.emit("__syncthreads();")
+            if fast and os.environ.get("NEWT_BARE_BARRIER", "0") == "1":
+                self.emit("newt::barrier_nofence();")
+            else:
+                self.emit("__syncthreads();")
             self.emit("__builtin_amdgcn_sched_barrier(0);")
             if fast and state["exp_mix"] and os.environ.get("NEWT_IGLP", "1") != "0":
                 self.emit("__builtin_amdgcn_iglp_opt(2);")

@@ -79,6 +79,17 @@ __device__ __forceinline__ void load_vec(const T* __restrict__ p, T* out) {
   for (int i = 0; i < N; ++i) out[i] = v.d[i];
 }
 
+// load_vec with the non-temporal hint (global_load ... nt): for data that
+// no other program reads, so its lines need not stay in the caches.
+template <typename T, int N>
+__device__ __forceinline__ void load_vec_nt(const T* __restrict__ p, T* out) {
+  typedef typename raw_vec<sizeof(T) * N>::type R;
+  R r = __builtin_nontemporal_load(reinterpret_cast<const R*>(p));
+  vec_t<T, N> v = __builtin_bit_cast(vec_t<T, N>, r);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = v.d[i];
+}
+
 template <typename T, int N>
 __device__ __forceinline__ void store_vec(T* __restrict__ p, const T* in) {
   typedef typename raw_vec<sizeof(T) * N>::type R;
@@ -462,6 +473,15 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
+
+// Workgroup barrier without the fence __syncthreads() carries. That fence
+// waits for all of this wave's LDS reads (lgkmcnt(0)) before the wave
+// arrives, including a fragment prefetch of a pipeline stage that the
+// barrier does not release. Callers wait for the copies the barrier publishes
+// (wait_vmcnt) first; reads of the stage the barrier releases have all been
+// consumed by then. The "memory" clobber keeps the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
 
 template <typename T> struct frag8;
 template <> struct frag8<f16> { typedef f16x8 type; };

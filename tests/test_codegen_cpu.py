@@ -72,6 +72,8 @@ def test_vector_add_layout_and_vector_path():
     assert "newt::load_vec<float, 4>" in src      # 16-byte fast path
     assert "newt::store_vec<float, 4>" in src
     assert "blockIdx.x" in src and "__restrict__" in src
+    # no program shares data with others: hardware workgroup order
+    assert "_pb" not in src
     assert lds == 0                               # pure elementwise: no LDS
     asm = isa(src)
     assert "global_load_dwordx4" in asm and "global_store_dwordx4" in asm
@@ -539,11 +541,53 @@ def test_matmul_tiles_are_stored_non_temporal(monkeypatch):
     asrc, _ = compile_source(W.attention_kernel, _attention_args(),
                              {"BLOCK_M": 128, "BLOCK_N": 64, "D": 128, "CAUSAL": False},
                              num_warps=4, num_stages=2)
-    assert "newt::store_vec<__bf16, 4>(" in asrc and "nontemporal" not in asrc
+    assert "newt::store_vec<__bf16, 4>(" in asrc and "nontemporal_store" not in asrc
     assert "store_vec_nt" not in asrc
     sm, _ = compile_source(W.softmax_kernel, {"x_ptr": (F32P, A16), "out_ptr": (F32P, A16),
                                               "N": (tp.int32, D16), "stride": (tp.int32, D16)},
                            {"BLOCK_N": 4096}, num_warps=4)
-    assert "nontemporal" not in sm and "store_vec_nt" not in sm
+    assert "nontemporal_store" not in sm and "store_vec_nt" not in sm
     monkeypatch.setenv("NEWT_NT_STORE", "0")
-    assert "nontemporal" not in mm()
+    assert "nontemporal_store" not in mm()
+
+
+def test_program_data_sharing_decides_order_and_hints(monkeypatch):
+    """Streaming kernels (every load private to its program or common to all)
+    keep the hardware's workgroup order; kernels whose programs share data
+    with a subset of the others (a matmul's panels, an attention head's keys)
+    are renumbered per XCD. NEWT_NT_LOAD=1 marks exactly the program-private
+    top-level loads non-temporal (a layernorm's x, not its weights)."""
+    import ast as _ast
+    from newt_amd.compiler import _shares_across_programs, _streamed
+    def parse(k):
+        return fndef_of(k)[0]
+    for k in (W.add_kernel, W.copy_kernel, W.softmax_kernel, W.layernorm_kernel):
+        assert not _shares_across_programs(parse(k)), k
+    for k in (W.matmul_kernel, W.attention_kernel, W.attention_plain_kernel):
+        assert _shares_across_programs(parse(k)), k
+        assert not _streamed(parse(k), ("load",)), k
+    ln = parse(W.layernorm_kernel)
+    streamed = _streamed(ln, ("load",))
+    loads = [n for n in _ast.walk(ln) if isinstance(n, _ast.Call)
+             and getattr(n.func, "attr", None) == "load"]
+    names = {_ast.unparse(n.args[0]).split(" ")[0]: id(n) in streamed for n in loads}
+    assert names == {"x_ptr": True, "w_ptr": False, "b_ptr": False}
+    monkeypatch.setenv("NEWT_NT_LOAD", "1")
+    src, _ = compile_source(W.layernorm_kernel, {
+        "x_ptr": (F16P, A16), "w_ptr": (F16P, A16), "b_ptr": (F16P, A16), "out_ptr": (F16P, A16),
+        "mean_ptr": (F32P, A16), "rstd_ptr": (F32P, A16), "N": tp.int32, "stride": tp.int32,
+        "eps": tp.float32}, {"BLOCK_N": 8192})
+    assert "newt::load_vec_nt<_Float16, 8>((_p" in src
+    assert "newt::load_vec<_Float16, 8>((w_ptr" in src and "newt::load_vec<_Float16, 8>((b_ptr" in src
+    assert re.search(r"global_load_dwordx4 .* nt", isa(src))
+    monkeypatch.delenv("NEWT_NT_LOAD")
+
+    def loop_reread(x_ptr, o_ptr, BLOCK: nl.constexpr):
+        row = nl.program_id(0)
+        acc = nl.zeros((BLOCK,), dtype=nl.float32)
+        for i in range(4):
+            acc += nl.load(x_ptr + row * BLOCK + nl.arange(0, BLOCK))
+        nl.store(o_ptr + row * BLOCK + nl.arange(0, BLOCK), acc)
+    fd = _ast.parse(textwrap.dedent(inspect.getsource(loop_reread))).body[0]
+    assert not _streamed(fd, ("load",))          # re-read in a loop: keep cached
+    assert _shares_across_programs(fd)           # a load in a loop: keep the XCD order

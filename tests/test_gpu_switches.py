@@ -22,7 +22,8 @@ SWITCHES = [
     ("NEWT_SCHED", "0"), ("NEWT_IGLP", "0"), ("NEWT_LDS_DMA", "0"), ("NEWT_BUFFER_DMA", "0"),
     ("NEWT_NT_STORE", "0"), ("NEWT_MFMA", "16"), ("NEWT_MFMA", "32"), ("NEWT_VEC", "1"),
     ("NEWT_VEC", "2"), ("NEWT_HOIST_LOADS", "1"), ("NEWT_PID_REMAP", "0"),
-    ("NEWT_PID_GROUP", "0"), ("NEWT_PID_GROUP", "2"),
+    ("NEWT_PID_GROUP", "0"), ("NEWT_PID_GROUP", "2"), ("NEWT_BARE_BARRIER", "1"),
+    ("NEWT_WHERE_VERSION", "0"), ("NEWT_NT_LOAD", "1"), ("NEWT_NT_STREAM", "1"),
 ]
 
 
