@@ -181,15 +181,101 @@ struct Min {
   template <typename T> __device__ __forceinline__ static T op(T a, T b) { return a < b ? a : b; }
 };
 
-// Butterfly over the lane bits set in MASK (compile-time), combining with Op.
+// DPP row mirrors: lane i of each 8-lane half row takes lane 7 - i
+// (row_half_mirror), of each 16-lane row lane 15 - i (row_mirror).
+template <int W>
+__device__ __forceinline__ int mirror_lane_i32(int v) {
+  static_assert(W == 8 || W == 16, "mirror width");
+  return __builtin_amdgcn_mov_dpp(v, W == 8 ? 0x141 : 0x140, 0xF, 0xF, true);
+}
+
+// Both members of the lane pair {l & ~M, l | M} (M = 16 or 32) in every lane,
+// from one v_permlane{16,32}_swap: swapping the odd rows (M = 16) or the upper
+// half (M = 32) of one copy of v with the even rows / lower half of another
+// leaves v[l & ~M] in the first copy and v[l | M] in the second.
+template <int M>
+__device__ __forceinline__ void pair_lanes_i32(int v, int& lo, int& hi) {
+  static_assert(M == 16 || M == 32, "pair mask");
+  if constexpr (M == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap((u32)v, (u32)v, false, false);
+    u32 a = r[0], b = r[1];
+    lo = (int)a;
+    hi = (int)b;
+  } else {
+    auto r = __builtin_amdgcn_permlane32_swap((u32)v, (u32)v, false, false);
+    u32 a = r[0], b = r[1];
+    lo = (int)a;
+    hi = (int)b;
+  }
+}
+
+template <int W, typename T>
+__device__ __forceinline__ T mirror_lane(T v) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, mirror_lane_i32<W>(__builtin_bit_cast(int, v)));
+  } else if constexpr (sizeof(T) == 8) {
+    u32x2 w = __builtin_bit_cast(u32x2, v);
+    w.x = (u32)mirror_lane_i32<W>((int)w.x);
+    w.y = (u32)mirror_lane_i32<W>((int)w.y);
+    return __builtin_bit_cast(T, w);
+  } else {
+    return (T)mirror_lane_i32<W>((int)v);
+  }
+}
+
+template <int M, typename T>
+__device__ __forceinline__ void pair_lanes(T v, T& lo, T& hi) {
+  if constexpr (sizeof(T) == 4) {
+    int a, b;
+    pair_lanes_i32<M>(__builtin_bit_cast(int, v), a, b);
+    lo = __builtin_bit_cast(T, a);
+    hi = __builtin_bit_cast(T, b);
+  } else if constexpr (sizeof(T) == 8) {
+    u32x2 w = __builtin_bit_cast(u32x2, v), l2, h2;
+    int a, b;
+    pair_lanes_i32<M>((int)w.x, a, b);
+    l2.x = (u32)a;
+    h2.x = (u32)b;
+    pair_lanes_i32<M>((int)w.y, a, b);
+    l2.y = (u32)a;
+    h2.y = (u32)b;
+    lo = __builtin_bit_cast(T, l2);
+    hi = __builtin_bit_cast(T, h2);
+  } else {
+    int a, b;
+    pair_lanes_i32<M>((int)v, a, b);
+    lo = (T)a;
+    hi = (T)b;
+  }
+}
+
+// Butterfly over the lane bits set in MASK (compile-time), combining with Op,
+// every step on the VALU (no LDS-pipe swizzle or bpermute) where it can be:
+//   bits 0, 1: DPP quad_perm (the xor partner);
+//   bit 2 (3): once bits 0-1 (0-2) are reduced, all lanes of a 4- (8-) lane
+//     group hold the same value, so the half-row (row) mirror partner, which
+//     lies in the other group, gives exactly what the xor partner would;
+//     otherwise ds_swizzle's xor;
+//   bits 4, 5: the permlane swaps, combining op(v[l & ~M], v[l | M]) in every
+//     lane (the xor pair, in one operand order for all lanes).
 template <typename Op, int MASK, typename T>
 __device__ __forceinline__ T lane_reduce(T v) {
   if constexpr (MASK & 1) v = Op::op(v, xor_lane<1>(v));
   if constexpr (MASK & 2) v = Op::op(v, xor_lane<2>(v));
-  if constexpr (MASK & 4) v = Op::op(v, xor_lane<4>(v));
-  if constexpr (MASK & 8) v = Op::op(v, xor_lane<8>(v));
-  if constexpr (MASK & 16) v = Op::op(v, xor_lane<16>(v));
-  if constexpr (MASK & 32) v = Op::op(v, xor_lane<32>(v));
+  if constexpr ((MASK & 7) == 7) v = Op::op(v, mirror_lane<8>(v));
+  else if constexpr (MASK & 4) v = Op::op(v, xor_lane<4>(v));
+  if constexpr ((MASK & 15) == 15) v = Op::op(v, mirror_lane<16>(v));
+  else if constexpr (MASK & 8) v = Op::op(v, xor_lane<8>(v));
+  if constexpr (MASK & 16) {
+    T lo, hi;
+    pair_lanes<16>(v, lo, hi);
+    v = Op::op(lo, hi);
+  }
+  if constexpr (MASK & 32) {
+    T lo, hi;
+    pair_lanes<32>(v, lo, hi);
+    v = Op::op(lo, hi);
+  }
   return v;
 }
 

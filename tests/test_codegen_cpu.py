@@ -101,7 +101,11 @@ def test_softmax_wave64_reductions():
     assert lds > 0                                # cross-wave partials go through LDS
     asm = isa(src)
     assert "quad_perm" in asm                     # DPP steps
-    assert "ds_swizzle_b32" in asm
+    # a whole-wave butterfly stays on the VALU: DPP mirrors for lane bits 2-3,
+    # permlane swaps for bits 4-5, nothing through the LDS pipe
+    assert "row_half_mirror" in asm and "row_mirror" in asm
+    assert "v_permlane16_swap_b32" in asm and "v_permlane32_swap_b32" in asm
+    assert "ds_swizzle_b32" not in asm and "ds_bpermute_b32" not in asm
 
 
 def test_layernorm_fp16_io_fp32_math():

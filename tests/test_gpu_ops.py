@@ -361,6 +361,44 @@ def test_reduce_axis(op, axis, mn):
 
 
 @newt.jit
+def reduce2d_whole_k(x_ptr, o_ptr, OP: nl.constexpr, AXIS: nl.constexpr,
+                     BM: nl.constexpr, BN: nl.constexpr):
+    rm = nl.arange(0, BM)
+    rn = nl.arange(0, BN)
+    v = nl.load(x_ptr + rm[:, None] * BN + rn[None, :])
+    if OP == "sum":
+        r = nl.sum(v, axis=AXIS)
+    elif OP == "max":
+        r = nl.max(v, axis=AXIS)
+    else:
+        r = nl.min(v, axis=AXIS)
+    if AXIS == 0:
+        nl.store(o_ptr + rn, r)
+    else:
+        nl.store(o_ptr + rm, r)
+
+
+@pytest.mark.parametrize("waves", [1, 2, 4])
+@pytest.mark.parametrize("mn", [(2, 32), (4, 16), (8, 8), (16, 4), (32, 2), (64, 1), (1, 64),
+                                (2, 128), (128, 2), (16, 64), (64, 16), (256, 8), (8, 256)])
+@pytest.mark.parametrize("dt", [torch.int32, torch.int64])
+def test_reduce_axis_exact_int(dt, mn, waves):
+    # every split of a block's axes over lane bits (so each partial lane mask of
+    # the wave64 butterfly, 4- and 8-byte values): integer results are exact
+    M, N = mn
+    g = torch.Generator().manual_seed(M * 1000 + N)
+    x = torch.randint(-10**6, 10**6, (M, N), generator=g, dtype=dt).cuda()
+    if dt == torch.int64:
+        x = x * (1 << 20)                         # uses the upper word
+    for axis in (0, 1):
+        for op in ("sum", "max", "min"):
+            o = torch.empty(N if axis == 0 else M, device="cuda", dtype=dt)
+            reduce2d_whole_k[(1,)](x, o, OP=op, AXIS=axis, BM=M, BN=N, num_warps=waves)
+            want = {"sum": x.sum(axis), "max": x.amax(axis), "min": x.amin(axis)}[op]
+            assert torch.equal(o, want.to(dt)), (op, axis)
+
+
+@newt.jit
 def reduce_full_k(x_ptr, o_ptr, n, OP: nl.constexpr, BLOCK: nl.constexpr):
     offs = nl.arange(0, BLOCK)
     live = offs < n
