@@ -74,6 +74,18 @@ def _target(s):
     return None
 
 
+def _targets(s):
+    """Names a statement of a pipelined body assigns (a runtime `if` assigns
+    those of both branches)."""
+    if isinstance(s, ast.If):
+        out = set()
+        for x in s.body + s.orelse:
+            out |= _targets(x)
+        return out
+    nm = _target(s)
+    return {nm} if nm is not None else set()
+
+
 def _operand_name(a):
     """(name, transposed) of a dot operand written `x`, `nl.trans(x)` or `x.T`."""
     trans = False
@@ -155,13 +167,34 @@ class DotPipeline:
             return None if v is None else not v
         return None
 
+    def _branch_ok(self, stmts):
+        """A runtime `if` inside a pipelined body holds plain assignments (and
+        such `if`s) only: no load, dot or side effect, so the stages' copies
+        and the dots' operands never depend on the branch taken."""
+        for s in stmts:
+            if isinstance(s, ast.If):
+                if not (self._branch_ok(s.body) and self._branch_ok(s.orelse)):
+                    return False
+            elif isinstance(s, (ast.Assign, ast.AugAssign, ast.AnnAssign)):
+                if _target(s) is None or getattr(s, "value", None) is None:
+                    return False
+            elif not isinstance(s, ast.Pass):
+                return False
+            if any(_callee(n) in _SIDE_EFFECTS | {"load", "dot"} for n in ast.walk(s)):
+                return False
+        return True
+
     def _flatten(self, stmts):
         out = []
         for s in stmts:
             if isinstance(s, ast.If):
                 v = self._const_test(s.test)
                 if v is None:
-                    return None
+                    # a runtime branch stays one statement of the body
+                    if not self._branch_ok([s]):
+                        return None
+                    out.append(s)
+                    continue
                 sub = self._flatten(s.body if v else s.orelse)
                 if sub is None:
                     return None
@@ -190,7 +223,8 @@ class DotPipeline:
                 return None
         assigned = {}
         for i, s in enumerate(flat):
-            assigned.setdefault(_target(s), []).append(i)
+            for nm in _targets(s):
+                assigned.setdefault(nm, []).append(i)
         if kname in assigned:
             return None
         uses = {}
@@ -227,7 +261,7 @@ class DotPipeline:
         konly = set()
         for s in flat:
             nm = _target(s)
-            if nm in carried or len(assigned[nm]) != 1 or not isinstance(s, ast.Assign):
+            if nm is None or nm in carried or len(assigned[nm]) != 1 or not isinstance(s, ast.Assign):
                 continue
             if any(_callee(n) in ("load", "dot") for n in ast.walk(s.value)):
                 continue
@@ -929,7 +963,7 @@ class DotPipeline:
         """Load A operands that do not change in the loop into MFMA operand
         registers once, before it."""
         plan = state["plan"]
-        assigned = {_target(s) for s in plan["flat"]}
+        assigned = set().union(*(_targets(s) for s in plan["flat"]))
         for s in plan["flat"]:
             for nd in ast.walk(s):
                 if _callee(nd) != "dot" or len(nd.args) < 2:

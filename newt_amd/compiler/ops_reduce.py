@@ -16,6 +16,7 @@ statistic of an MFMA tile stays one-row-per-lane and broadcasts back for free.
 """
 
 import math
+import os
 
 from . import types as tp
 from .values import Block, Const, LazyLoad, Reg, Scalar
@@ -58,9 +59,26 @@ class ReduceOps:
         return self._reduce_full(x, op, rt)
 
     def _lds_for_reduce(self, nbytes):
-        if self.loop_depth:
+        """LDS offset (a C expression) for one reduction site's cross-wave
+        partials. Outside loops the site has one region. Inside a loop it runs
+        again, so a write must not overtake a slower wave's reads of the last
+        partials: the site alternates between two regions, and the barrier
+        that follows each write (which a wave reaches only after reading the
+        site's previous partials, in program order) then separates every
+        write from the reads of the same region two executions back, with no
+        barrier before the write. Large partial sets keep one region and a
+        barrier before the write."""
+        if not self.loop_depth:
+            return self.lds_alloc(nbytes)
+        if nbytes > 4096 or os.environ.get("NEWT_REDUCE_PINGPONG", "1") == "0":
             self.barrier()
-        return self.lds_alloc(nbytes)
+            return self.lds_alloc(nbytes)
+        stride = (nbytes + 15) // 16 * 16
+        region = self.lds_alloc(2 * stride)
+        par = self.fresh("rpar")
+        self.prologue.append(f"unsigned {par} = 0u;")
+        self.emit(f"{par} ^= 1u;")
+        return f"({region} + {par} * {stride}u)"
 
     def _reduce_full(self, x, op, rt):
         L = x.layout

@@ -255,18 +255,28 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
     if CAUSAL:
         full_n = nl.minimum(full_n, pid * BLOCK_M // BLOCK_N * BLOCK_N)
         end_n = nl.minimum(S, (pid + 1) * BLOCK_M)
+    #
+    # The running maximum m_i moves only when some row's block maximum passes
+    # it by more than 8 (in log2 units): until then p = exp2(qk * s - m_i)
+    # stays <= 2^8, and acc and l_i keep their scale, so the per-block
+    # rescale of acc (64 multiplies per lane) runs only on the blocks that
+    # move it (the first, and rarely another). O = acc / l_i is the same
+    # quotient whichever reference point the exponents share.
     for start_n in range(0, full_n, BLOCK_N):
         offs_n = start_n + nl.arange(0, BLOCK_N)
         k = nl.load(k_base + offs_n[:, None] * skn + offs_d[None, :])
         qk = nl.dot(q, nl.trans(k))
-        m_new = nl.maximum(m_i, nl.max(qk, axis=1) * qk_scale)
-        alpha = nl.exp2(m_i - m_new)
-        p = nl.exp2(nl.fma(qk, qk_scale, -m_new[:, None]))
-        l_i = l_i * alpha + nl.sum(p, axis=1)
-        acc = acc * alpha[:, None]
+        m_blk = nl.max(qk, axis=1) * qk_scale
+        if nl.max(m_blk - m_i) > 8.0:
+            m_new = nl.maximum(m_i, m_blk)
+            alpha = nl.exp2(m_i - m_new)
+            l_i = l_i * alpha
+            acc = acc * alpha[:, None]
+            m_i = m_new
+        p = nl.exp2(nl.fma(qk, qk_scale, -m_i[:, None]))
+        l_i = l_i + nl.sum(p, axis=1)
         v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :])
         acc = nl.dot(p.to(v_ptr.dtype.element_ty), v, acc)
-        m_i = m_new
     for start_n in range(full_n, end_n, BLOCK_N):
         offs_n = start_n + nl.arange(0, BLOCK_N)
         nmask = offs_n[:, None] < S
@@ -277,14 +287,20 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
                           qk, float("-inf"))
         else:
             qk = nl.where(offs_n[None, :] < S, qk, float("-inf"))
-        m_new = nl.maximum(m_i, nl.max(qk, axis=1) * qk_scale)
-        alpha = nl.exp2(m_i - m_new)
-        p = nl.exp2(nl.fma(qk, qk_scale, -m_new[:, None]))
-        l_i = l_i * alpha + nl.sum(p, axis=1)
-        acc = acc * alpha[:, None]
+        # a row whose keys are all masked here has m_blk = -inf: it never
+        # moves the maximum, and its p is exp2(-inf) = 0 (every row has a
+        # finite m_i from the first key block on: key 0 is never masked)
+        m_blk = nl.max(qk, axis=1) * qk_scale
+        if nl.max(m_blk - m_i) > 8.0:
+            m_new = nl.maximum(m_i, m_blk)
+            alpha = nl.exp2(m_i - m_new)
+            l_i = l_i * alpha
+            acc = acc * alpha[:, None]
+            m_i = m_new
+        p = nl.exp2(nl.fma(qk, qk_scale, -m_i[:, None]))
+        l_i = l_i + nl.sum(p, axis=1)
         v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :], mask=nmask, other=0.0)
         acc = nl.dot(p.to(v_ptr.dtype.element_ty), v, acc)
-        m_i = m_new
 
     acc = acc / l_i[:, None]
     nl.store(o_base + offs_m[:, None] * som + offs_d[None, :], acc.to(o_ptr.dtype.element_ty),

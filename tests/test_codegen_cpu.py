@@ -447,7 +447,9 @@ def test_sequential_pipelined_loops_share_lds_stages():
         src, lds = compile_source(W.attention_kernel, args,
                                   {"BLOCK_M": 128, "BLOCK_N": 64, "D": 128, "CAUSAL": causal},
                                   num_warps=4, num_stages=2, waves_per_eu=2)
-        assert lds == 64 * 1024
+        # + the cross-wave partials of the maximum test (two buffers per loop):
+        # two programs still fit one CU's 160 KiB
+        assert 64 * 1024 <= lds <= 64 * 1024 + 1024
         assert len(re.findall(r"for \(; _it\d+ \+ 2 <", src)) == 2   # two fast copies
         assert src.count("newt::lds_dma16(") >= 16
 

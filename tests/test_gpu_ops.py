@@ -399,6 +399,49 @@ def test_reduce_axis_exact_int(dt, mn, waves):
 
 
 @newt.jit
+def reduce_in_loop_k(x_ptr, part_ptr, col_ptr, o_ptr, ITERS: nl.constexpr,
+                     BM: nl.constexpr, BN: nl.constexpr):
+    rm = nl.arange(0, BM)
+    rn = nl.arange(0, BN)
+    total = 0
+    cols = nl.zeros((BN,), dtype=nl.int32)
+    for i in range(0, ITERS):
+        v = nl.load(x_ptr + i * BM * BN + rm[:, None] * BN + rn[None, :])
+        s = nl.sum(v)                       # across every wave, each iteration
+        nl.store(part_ptr + i, s)
+        if nl.max(v) > 0:                   # a branch on a cross-wave reduction
+            total = total + s
+        cols = cols + nl.max(v, axis=0)     # across the waves holding rows
+    nl.store(o_ptr, total)
+    nl.store(col_ptr + rn, cols)
+
+
+@pytest.mark.parametrize("waves", [2, 4, 8])
+@pytest.mark.parametrize("bm_bn", [(64, 64), (256, 16), (16, 256)])
+def test_cross_wave_reductions_in_a_loop(bm_bn, waves):
+    # every iteration reduces across the waves through LDS; consecutive
+    # iterations alternate between two partial buffers with no barrier ahead
+    # of the write: exact integer results over many iterations pin that no
+    # wave reads partials a faster wave has already overwritten
+    BM, BN = bm_bn
+    iters = 37
+    g = torch.Generator().manual_seed(BM + BN + waves)
+    x = torch.randint(-1000, 1000, (iters, BM, BN), generator=g, dtype=torch.int32)
+    x[5] = -x[5].abs() - 1                 # an iteration whose branch is not taken
+    x = x.cuda()
+    part = torch.empty(iters, device="cuda", dtype=torch.int32)
+    col = torch.empty(BN, device="cuda", dtype=torch.int32)
+    o = torch.empty(1, device="cuda", dtype=torch.int32)
+    reduce_in_loop_k[(1,)](x, part, col, o, ITERS=iters, BM=BM, BN=BN, num_warps=waves)
+    xs = x.cpu().long()
+    sums = xs.sum((1, 2))
+    assert part.cpu().long().tolist() == sums.tolist()
+    keep = xs.amax((1, 2)) > 0
+    assert int(o.item()) == int(sums[keep].sum())
+    assert col.cpu().long().tolist() == xs.amax(1).sum(0).tolist()
+
+
+@newt.jit
 def reduce_full_k(x_ptr, o_ptr, n, OP: nl.constexpr, BLOCK: nl.constexpr):
     offs = nl.arange(0, BLOCK)
     live = offs < n
