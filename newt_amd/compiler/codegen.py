@@ -178,6 +178,10 @@ class Codegen(ast.NodeVisitor):
         self.new_hints = {}
         self.lines = []
         self.prologue = []
+        self._blocks = []       # ids of the open C blocks, outermost first
+        self._block_seq = 0
+        self.cse = {}           # binop key -> (operands, result Reg, C block path)
+        self.cse_on = os.environ.get("NEWT_CSE", "1") != "0"
         self.indent = 1
         self.tmpc = 0
         self.locals = {}
@@ -220,6 +224,42 @@ class Codegen(ast.NodeVisitor):
             self.locals[name] = Const(v)
 
     # ------------------------------------------------------------------ infra
+    @property
+    def indent(self):
+        return len(self._blocks)
+
+    @indent.setter
+    def indent(self, depth):
+        """Every increase opens a new C block (a fresh id), every decrease
+        closes the innermost ones; `} else {` therefore gets an id of its own."""
+        del self._blocks[depth:]
+        while len(self._blocks) < depth:
+            self._block_seq += 1
+            self._blocks.append(self._block_seq)
+
+    def cse_lookup(self, key, operands):
+        """A register block computed earlier from the same operand objects by
+        the same operation, if its C declaration is visible here."""
+        hit = self.cse.get(key)
+        if hit is None:
+            return None
+        ops, res, path = hit
+        if len(ops) != len(operands) or any(x is not y for x, y in zip(ops, operands)):
+            return None
+        if tuple(self._blocks[:len(path)]) != path:
+            return None
+        return res
+
+    def cse_store(self, key, operands, res):
+        """Remember res for reuse: only materialized, immutable register
+        blocks whose operands are not loop-carried storage (storage is
+        rewritten in place; every read of it is a new object anyway)."""
+        if not isinstance(res, Reg) or res.storage or not self.cse_on:
+            return
+        if any(isinstance(o, Reg) and o.storage for o in operands):
+            return
+        self.cse[key] = (tuple(operands), res, tuple(self._blocks))
+
     def err(self, node, msg):
         line = getattr(node, "lineno", "?")
         raise CompileError(f"{self.fndef.name}:{line}: {msg}")
@@ -1324,6 +1364,18 @@ class Codegen(ast.NodeVisitor):
                 if sym.is_const:
                     return self.new_scalar(rd, self.literal(sym.const, rd), sym)
                 return self.new_scalar(rd, self.conv(sym.expr, None, None), sym)
+        # the same operation on the same operand objects reuses the earlier
+        # register block: `(x - mean)` written twice (layernorm's variance and
+        # output) is computed once, and x need not stay live for the second
+        key = ("bin", op, rd, id(a), id(b))
+        hit = self.cse_lookup(key, (a, b))
+        if hit is not None:
+            return hit
+        r = self._binop_values(node, op, a, b, rd)
+        self.cse_store(key, (a, b), r)
+        return r
+
+    def _binop_values(self, node, op, a, b, rd):
         half = tp.is_half(rd)
         cd = tp.compute_dtype(rd)
 

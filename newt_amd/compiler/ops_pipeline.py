@@ -399,7 +399,10 @@ class DotPipeline:
         self.emit(f"{idt.ctype} {it0} = 0;")
         mark = len(self.lines)
         ctx = (node, state, S, n, lo_e, stv, idt, slice_stmts, advance, skip, temps, kname, flat)
+        state["clamp"] = os.environ.get("NEWT_PIPE_CLAMP", "1") != "0"
+        state["clamp_n"] = n
         if plan["fast_ok"] and os.environ.get("NEWT_PIPE_VERSION", "1") != "0":
+            state["fast_emitted"] = True
             # leading iterations whose every tile is a whole in-bounds copy run
             # in a copy of the loop with no per-iteration tests at all; its
             # copies take the buffer form (32-bit lane offsets) when every
@@ -409,9 +412,27 @@ class DotPipeline:
             self.emit(f"for (; {it0} + {2 * S - 2} < {nf.expr}; {it0} += {S}) {{")
             self._pipe_iterations(ctx, it0, fast=True)
             self.emit("}")
+            if state["clamp"]:
+                # when every iteration is fast, one more branch-free trip runs
+                # S of the last iterations: its copies past the end repeat the
+                # last tile into stages no iteration reads again, so every
+                # sub-iteration keeps the same copies in flight and the same
+                # waits (the general loop ran these ~1.5x slower). The loop
+                # above stays as it was: clamping there lengthened the scalar
+                # work ahead of every copy.
+                self.emit(f"if ((({nf.expr}) == ({n.expr})) && {it0} + {S - 1} < {n.expr}) {{")
+                state["clamp_trip"] = True
+                self._pipe_iterations(ctx, it0, fast=True)
+                state["clamp_trip"] = False
+                self.emit(f"  {it0} += {S};")
+                self.emit("}")
         self.emit(f"for (; {it0} < {n.expr}; {it0} += {S}) {{")
         self._pipe_iterations(ctx, it0, fast=False)
         self.emit("}")
+        if state.get("clamp") and state.get("fast_emitted"):
+            # repeated copies may still be in flight: drain them before the
+            # stages' LDS is reused or the workgroup ends
+            self.emit("newt::wait_vmcnt<0>();")
         if state["plr"]:
             self._insert_lines(mark, self._plr_preamble(state, n))
         self._exit_compound(rec)
@@ -617,10 +638,26 @@ class DotPipeline:
             if fast and state["exp_mix"] and os.environ.get("NEWT_IGLP", "1") != "0":
                 self.emit("__builtin_amdgcn_iglp_opt(2);")
             # issue iteration it+S-1 into the stage that iteration it-1 read
-            self.locals[kname] = self.new_scalar(idt, f"({lo_e} + ({it} + {S - 1}) * {stv})")
+            issue = f"({it} + {S - 1})"
+            clamp = fast and state.get("clamp_trip", False)
+            if clamp:
+                # past the last iteration the branch-free copy repeats the last
+                # tile, and the carried pointers stay on it
+                last = f"({n.expr} - 1)"
+                self.locals[kname] = self.new_scalar(
+                    idt, f"({lo_e} + (({issue} < {last}) ? {issue} : {last}) * {stv})")
+            else:
+                self.locals[kname] = self.new_scalar(idt, f"({lo_e} + {issue} * {stv})")
             self.visit_body(slice_stmts)
-            self.pipe_issue(state, (s + S - 1) % S, f"({it} + {S - 1} < {n.expr})", fast=fast)
-            self.visit_body(advance)
+            self.pipe_issue(state, (s + S - 1) % S, f"({issue} < {n.expr})", fast=fast)
+            if clamp and advance:
+                self.emit(f"if ({issue} < {n.expr} - 1) {{")
+                self.indent += 1
+                self.visit_body(advance)
+                self.indent -= 1
+                self.emit("}")
+            else:
+                self.visit_body(advance)
             for t in temps:
                 self.locals.pop(t, None)
             # compute iteration it from stage s

@@ -484,7 +484,8 @@ def test_fast_loop_copies_take_the_buffer_form(monkeypatch):
     loops = [m.start() for m in re.finditer(r"for \(; _it\d+ ", src)]
     assert len(loops) == 2
     before, fast, general = src[:loops[0]], src[loops[0]:loops[1]], src[loops[1]:]
-    assert fast.count("newt::lds_dma16_buf(") == 32 and "newt::lds_dma16(" not in fast
+    # the fast loop and the one clamped trip after it, 8 copies per sub-iteration each
+    assert fast.count("newt::lds_dma16_buf(") == 64 and "newt::lds_dma16(" not in fast
     assert "lds_dma16_buf" not in before and "lds_dma16_buf" not in general
     # the entry test reads the tiles' offsets without emitting their loads
     assert "? a_ptr[" not in fast and "? b_ptr[" not in fast
@@ -510,7 +511,8 @@ def test_fast_loop_fills_are_spaced_evenly_over_the_mfmas():
     loops = [m.start() for m in re.finditer(r"for \(; _it\d+ ", src)]
     fast = src[loops[0]:loops[1]]
     seq = re.findall(r"sched_group_barrier\((0x\w+), 1, 0\)", fast)
-    assert len(seq) == 4 * 96                       # 4 stages x (64 MFMAs + 32 fills)
+    # 4 stages x (64 MFMAs + 32 fills), in the loop and in the clamped trip after it
+    assert len(seq) == 2 * 4 * 96
     first = seq[:96]
     after = []
     for mask in first:
@@ -597,3 +599,71 @@ def test_program_data_sharing_decides_order_and_hints(monkeypatch):
     fd = _ast.parse(textwrap.dedent(inspect.getsource(loop_reread))).body[0]
     assert not _streamed(fd, ("load",))          # re-read in a loop: keep cached
     assert _shares_across_programs(fd)           # a load in a loop: keep the XCD order
+
+
+LN_ARGS = {"x_ptr": (F16P, A16), "w_ptr": (F16P, A16), "b_ptr": (F16P, A16),
+           "out_ptr": (F16P, A16), "mean_ptr": (F32P, A16), "rstd_ptr": (F32P, A16),
+           "N": (tp.int32, D16), "stride": (tp.int32, D16), "eps": tp.float32}
+
+
+def test_repeated_binop_is_computed_once(monkeypatch):
+    """layernorm writes `x - mean` for the variance and again for the output:
+    the second use takes the first block's registers (x - mean is evaluated
+    once per element), and NEWT_CSE=0 restores the recomputation."""
+    sub = re.compile(r"= \(\(\(float\)\(_r\d+\[0\]\)\) - _t\d+\);")
+    src, _ = compile_source(W.layernorm_kernel, LN_ARGS, {"BLOCK_N": 8192})
+    assert len(sub.findall(src)) == 1
+    isa(src)
+    monkeypatch.setenv("NEWT_CSE", "0")
+    src0, _ = compile_source(W.layernorm_kernel, LN_ARGS, {"BLOCK_N": 8192})
+    assert len(sub.findall(src0)) == 2
+
+
+def test_reuse_respects_c_scopes():
+    """A block computed inside a runtime `if` (or a loop body) is not visible
+    after it: the same expression there is computed again, and the source
+    builds. Values read from loop-carried storage are never reused across a
+    write of that storage."""
+    def k(x_ptr, o_ptr, flag, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        x = nl.load(x_ptr + offs)
+        y = x * 0.0
+        if flag > 0:
+            y = x * 3.0
+        z = x * 3.0
+        acc = x * 1.0
+        for i in range(3):
+            acc = acc * 2.0
+            t = acc * 2.0
+            acc = t + 1.0
+        nl.store(o_ptr + offs, y + z + acc)
+    src, _ = compile_source(k, {"x_ptr": (F32P, A16), "o_ptr": (F32P, A16), "flag": tp.int32},
+                            {"BLOCK": 256})
+    mul3 = re.findall(r"\* 3\.0f\)", src)
+    assert len(mul3) >= 2            # once in the branch, once after it
+    assert len(re.findall(r"\* 2\.0f\)", src)) >= 2   # both products of the loop body
+    isa(src)
+
+
+def test_fast_loop_runs_the_last_trips_with_repeated_copies(monkeypatch):
+    """When every iteration is fast, one more branch-free trip follows the
+    fast loop: its copies past the end repeat the last tile (clamped loop
+    variable), the carried pointers stop on it, and the copies are drained
+    after the loops. The fast loop itself is unchanged; NEWT_PIPE_CLAMP=0
+    drops the extra trip."""
+    cex = {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}
+    src, _ = compile_source(W.matmul_kernel, _matmul_args(), cex, num_warps=4, num_stages=4)
+    loops = [m.start() for m in re.finditer(r"for \(; _it\d+ ", src)]
+    assert len(loops) == 2
+    m = re.search(r"if \(\(\((_t\d+)\) == \((_t\d+)\)\) && (_it\d+) \+ 3 < \2\) \{", src)
+    assert m and loops[0] < m.start() < loops[1], "one clamped trip between the loops"
+    trip = src[m.start():loops[1]]
+    assert trip.count("newt::lds_dma16_buf(") == 32
+    assert re.search(r"if \(\(\(_it\d+ \+ 0\) \+ 3\) < _t\d+ - 1\) \{", trip)
+    assert f"{m.group(3)} += 4;" in trip
+    fast = src[loops[0]:m.start()]
+    assert "- 1) ?" not in fast and " - 1) {" not in fast    # no clamping in the loop
+    assert "newt::wait_vmcnt<0>();" in src[loops[1]:]
+    monkeypatch.setenv("NEWT_PIPE_CLAMP", "0")
+    src0, _ = compile_source(W.matmul_kernel, _matmul_args(), cex, num_warps=4, num_stages=4)
+    assert not re.search(r"\) && _it\d+ \+ 3 < ", src0)
