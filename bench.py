@@ -65,7 +65,16 @@ def parse():
     ap.add_argument("--only", default=None,
                     help="run one workload for profiler runs: 'matmul', 'copy', or the "
                          "start of a secondary workload's name (e.g. 'softmax fp32 4096x4096')")
-    return ap.parse_args()
+    ap.add_argument("--operands", default="random", choices=("random", "constant", "bf16-values"),
+                    help="with --only matmul: the configuration's N(0,1)/sqrt(K) operands "
+                         "(random), every element 1/64 (constant), or the random values "
+                         "rounded to bf16 first; the power the matrix cores draw, and so the "
+                         "clock the chip holds, depends on the operands' bits")
+    args = ap.parse_args()
+    if args.operands != "random" and args.only != "matmul":
+        ap.error("--operands applies to --only matmul runs (the headline uses the "
+                 "configuration's random operands)")
+    return args
 
 
 def seeded(shape, seed, scale=1.0, mean=0.0, dtype=None):
@@ -345,6 +354,12 @@ def main():
     S = args.size
     a = seeded((S, S), 4, scale=S ** -0.5, dtype=torch.float16)
     b = seeded((S, S), 5, scale=S ** -0.5, dtype=torch.float16)
+    if args.operands == "constant":
+        a.fill_(1 / 64)
+        b.fill_(1 / 64)
+    elif args.operands == "bf16-values":
+        a.copy_(a.bfloat16())
+        b.copy_(b.bfloat16())
     c = torch.empty(S, S, device="cuda", dtype=torch.float16)
     cfg = pick_matmul_config(a, b, c, args)
     step = lambda: W.matmul(a, b, c, config=cfg)
@@ -386,7 +401,8 @@ def main():
     # beside it: the events put ~8 us between launches and change the clocks
     achieved = flop / (total_ms / args.steps * 1e-3) / 1e12
     if args.only:
-        log(f"matmul only: {value:.1f} TFLOP/s")
+        log(f"matmul only ({args.operands} operands): {value:.1f} TFLOP/s, "
+            f"{statistics.median(kern_list) * 1e3:.2f} us per launch with dispatch events")
         return
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
