@@ -738,6 +738,11 @@ class Codegen(ast.NodeVisitor):
         lds_total = arena_off + self.arena_bytes
         lds_all = lds_total + sum(b for _, b in self.lds_arrays)
         if lds_all > MAX_LDS:
+            # layouts learned in this pass remove conversions (and their LDS)
+            # in the next one: try that before a pipeline gives anything up
+            if any(self.hints.get(k) != v for k, v in self.new_hints.items()
+                   if isinstance(v, lo.Layout)):
+                raise _Retry()
             # a dot pipeline that does not fit gives up a stage (down to 2), then
             # falls back to synchronous staging, before the kernel is rejected
             for rec in self.pipe_records:

@@ -667,3 +667,19 @@ def test_fast_loop_runs_the_last_trips_with_repeated_copies(monkeypatch):
     monkeypatch.setenv("NEWT_PIPE_CLAMP", "0")
     src0, _ = compile_source(W.matmul_kernel, _matmul_args(), cex, num_warps=4, num_stages=4)
     assert not re.search(r"\) && _it\d+ \+ 3 < ", src0)
+
+
+def test_layout_hints_before_pipeline_fallback():
+    """A first pass whose layout conversions push the LDS past 160 KB (flash
+    attention with 64 query rows per wave: its accumulator starts in a blocked
+    layout) is retried with the layouts it learned before the dot pipeline gives
+    up a stage or falls back to synchronous staging: the kernel keeps its two
+    direct-to-LDS stages and needs no conversion arena."""
+    args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
+    args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})
+    for n in ("sqb", "sqh", "sqm", "skb", "skh", "skn", "svb", "svh", "svn", "sob", "soh", "som"):
+        args[n] = (tp.int32, D16)
+    src, lds = compile_source(W.attention_kernel, args,
+                              {"BLOCK_M": 256, "BLOCK_N": 32, "D": 128, "CAUSAL": False},
+                              num_warps=4, num_stages=2, waves_per_eu=1)
+    assert lds < 2 * 16384 + 1024 and "lds_dma16_buf" in src
