@@ -904,8 +904,11 @@ class Codegen(ast.NodeVisitor):
         assigns the same name starts fresh instead of carrying a stale value."""
         self.pending_hoist.remove(rec)
         for name in _Prepass.assigned(rec["node"]) - rec["pre"] - rec["names"]:
-            if name not in self.storages:
-                self.locals.pop(name, None)
+            # a storage such a name got inside the statement (a loop nested in
+            # it carried the name) is declared in the same C block, so it goes
+            # out of scope with it as well
+            self.storages.pop(name, None)
+            self.locals.pop(name, None)
 
     def visit_For(self, node):
         self.flush_loads()

@@ -14,6 +14,7 @@ that need a launch, with the same known answers:
   broadcast_to of a uniform scalar                                        :238-247
   `other` may itself be a loaded block                                    :250-263
   uint32 tensors                                                          :276-285
+  a name carried by a loop inside a runtime if and assigned again after it
 The compile-time rejections of the same suite run on the CPU
 (test_language_errors_cpu.py).
 """
@@ -268,3 +269,30 @@ def test_cpu_tensor_rejected():
 
     with pytest.raises(TypeError, match="GPU tensor"):
         k[(1,)](torch.zeros(64), BLOCK=64)
+
+
+def test_name_carried_by_a_loop_inside_a_runtime_if_then_reassigned():
+    """A name first defined inside a runtime `if`, carried by a loop nested in
+    it, and assigned again after the `if`: the loop's storage is scoped to the
+    `if` block, and the later assignment starts a fresh value (the generated
+    source used to write the out-of-scope storage and failed to compile)."""
+    @newt.jit
+    def k(x_ptr, o_ptr, n, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        acc = nl.zeros((BLOCK,), dtype=nl.float32)
+        if n > 0:
+            t = nl.load(x_ptr + offs)
+            for i in range(1, n):
+                t = t + nl.load(x_ptr + offs + i)
+            acc = acc + t
+        t = nl.load(x_ptr + offs) * 2.0
+        nl.store(o_ptr + offs, acc + t)
+
+    x = torch.randn(300, device="cuda")
+    for n in (0, 1, 4):
+        o = torch.empty(256, device="cuda")
+        k[(1,)](x, o, n, BLOCK=256)
+        want = x[:256] * 2.0
+        if n > 0:
+            want = want + sum(x[i:i + 256] for i in range(n))
+        torch.testing.assert_close(o, want, rtol=1e-5, atol=1e-5)
