@@ -70,7 +70,13 @@ def parse():
                          "(random), every element 1/64 (constant), or the random values "
                          "rounded to bf16 first; the power the matrix cores draw, and so the "
                          "clock the chip holds, depends on the operands' bits")
+    ap.add_argument("--timeline", action="store_true",
+                    help="with --only matmul: per-workgroup start, end-of-k-loop and end "
+                         "timestamps of the headline kernel (s_memrealtime, 100 MHz), "
+                         "summarised per XCD")
     args = ap.parse_args()
+    if args.timeline and args.only != "matmul":
+        ap.error("--timeline applies to --only matmul runs")
     if args.operands != "random" and args.only != "matmul":
         ap.error("--operands applies to --only matmul runs (the headline uses the "
                  "configuration's random operands)")
@@ -363,6 +369,8 @@ def main():
     c = torch.empty(S, S, device="cuda", dtype=torch.float16)
     cfg = pick_matmul_config(a, b, c, args)
     step = lambda: W.matmul(a, b, c, config=cfg)
+    if args.timeline:
+        return matmul_timeline(a, b, c, cfg, step)
     # warm-up straight after the autotuner's runs: the chip's clocks drop
     # while it idles (a CPU-side check here cost ~20% on the first timed
     # launches), so the oracle check of the measured configuration's output
@@ -430,6 +438,85 @@ def main():
     if not args.no_secondary:
         out["secondary"] = secondary(cpu=not args.no_cpu)
     print(json.dumps(out), flush=True)
+
+
+def timeline_source(src):
+    """A generated matmul kernel's source with per-workgroup timestamps: one
+    more parameter, `unsigned long long* _ts` (4 values per workgroup: start,
+    end of the k-loop, end, XCC_ID), written by the workgroup's first thread."""
+    import re
+    head = re.search(r'extern "C" __global__ void [^{]*?\) \{', src)
+    src = (src[:head.end() - 3] + ", unsigned long long* __restrict__ _ts) {\n"
+           "  const unsigned long long _tsw_start = __builtin_amdgcn_s_memrealtime();" + src[head.end():])
+    lines = src.split("\n")
+    first = next(i for i, ln in enumerate(lines) if "c_ptr" in ln and "store" in ln)
+    while not (lines[first].startswith("  ") and not lines[first].startswith("   ")):
+        first -= 1   # the top-level statement holding the first C store
+    lines.insert(first, "  const unsigned long long _tsw_loop = __builtin_amdgcn_s_memrealtime();")
+    src = "\n".join(lines)
+    end = src.rstrip().rfind("}")
+    src = src[:end] + (
+        "  {\n"
+        "    const unsigned long long _tsw_end = __builtin_amdgcn_s_memrealtime();\n"
+        "    const unsigned int _tsw_xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20);\n"
+        "    if (threadIdx.x == 0) {\n"
+        "      const int _tsw_wg = blockIdx.x + gridDim.x * blockIdx.y;\n"
+        "      _ts[_tsw_wg * 4 + 0] = _tsw_start; _ts[_tsw_wg * 4 + 1] = _tsw_loop; _ts[_tsw_wg * 4 + 2] = _tsw_end;\n"
+        "      _ts[_tsw_wg * 4 + 3] = _tsw_xcc;\n"
+        "    }\n"
+        "  }\n") + src[end:]
+    return src
+
+
+def matmul_timeline(a, b, c, cfg, step, launches=40, keep=30):
+    """Per-workgroup timestamps of the headline matmul: a copy of the kernel's
+    generated source that reads the 100 MHz real-time counter at the start, at
+    the end of the k-loop (before the C tile's first store) and at the end,
+    and writes them with the workgroup's XCC_ID from its first thread. The
+    copy runs `launches` times back to back behind a GPU spin; the last `keep`
+    are summarised per XCD. Diagnostic only: the timed headline never runs it."""
+    import re
+    import torch
+    from newt_amd import workloads as W
+    from newt_amd.runtime import hip
+    S = a.shape[0]
+    args = (a, b, c, S, S, S, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
+            c.stride(0), c.stride(1))
+    ck = W.matmul_kernel.specialize(*args, **cfg.kwargs, num_warps=cfg.num_warps,
+                                    num_stages=cfg.num_stages)
+    src = timeline_source(ck.source)
+    kern = hip.Kernel(hip.compile_hip(src, ck.name), ck.name, ck.lds_bytes)
+    packer = hip.pack_format(ck.kinds + ["ptr"])
+    named = dict(zip(W.matmul_kernel.param_names, args))
+    vals = [named[n].data_ptr() if torch.is_tensor(named[n]) else named[n] for n in ck.param_names]
+    gx, gy = S // cfg.kwargs["BLOCK_M"], S // cfg.kwargs["BLOCK_N"]
+    bufs = [torch.zeros(gx * gy * 4, dtype=torch.int64, device="cuda") for _ in range(launches)]
+    stream = torch.cuda.current_stream().cuda_stream
+    for _ in range(50):
+        step()
+    settle_clocks(step, SETTLE_S)
+    torch.cuda._sleep(LEAD_CYCLES)
+    for buf in bufs:
+        kern.launch_packed(gx, gy, 1, 64 * cfg.num_warps, stream, packer.pack(*(vals + [buf.data_ptr()])))
+    torch.cuda.synchronize()
+    err, bad = check_matmul(a, b, c, "float16")
+    runs = [buf.view(-1, 4).cpu().tolist() for buf in bufs[-keep:]]
+    per = {}
+    for run in runs:
+        for t0, t1, t2, x in run:
+            d = per.setdefault(x & 0xF, {"loop": [], "store": []})
+            d["loop"].append((t1 - t0) / 100)
+            d["store"].append((t2 - t1) / 100)
+    spans = [(max(r[2] for r in run) - min(r[0] for r in run)) / 100 for run in runs]
+    starts = [(max(r[0] for r in run) - min(r[0] for r in run)) / 100 for run in runs]
+    log(f"matmul timeline: {keep} launches of {ck.name}, {gx * gy} workgroups each; "
+        f"rel. Frobenius {err:.2e}, {bad} elements beyond one ulp")
+    log(f"  launch span median {statistics.median(spans):.2f} us (workgroup start to last end); "
+        f"start spread median {statistics.median(starts):.2f} us")
+    for x in sorted(per):
+        lp, stv = per[x]["loop"], per[x]["store"]
+        log(f"  XCD {x}: {len(lp) // keep} workgroups, k-loop median {statistics.median(lp):.2f} us "
+            f"(min {min(lp):.2f}, max {max(lp):.2f}), C store median {statistics.median(stv):.2f} us")
 
 
 def run_only(name):

@@ -683,3 +683,17 @@ def test_layout_hints_before_pipeline_fallback():
                               {"BLOCK_M": 256, "BLOCK_N": 32, "D": 128, "CAUSAL": False},
                               num_warps=4, num_stages=2, waves_per_eu=1)
     assert lds < 2 * 16384 + 1024 and "lds_dma16_buf" in src
+
+
+def test_bench_timeline_source_compiles():
+    """bench.py --timeline instruments the headline matmul's generated source
+    (real-time counter reads at the start, before the first C store and at the
+    end, written with the XCC id through one more pointer parameter): the
+    instrumented copy must still build for gfx950."""
+    import bench
+    src, _ = compile_source(W.matmul_kernel, _matmul_args(F16P),
+                            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=4,
+                            num_stages=4)
+    inst = bench.timeline_source(src)
+    assert inst.count("s_memrealtime") == 3 and "_ts[_tsw_wg * 4 + 3]" in inst
+    assert "s_memrealtime" in isa(inst)
