@@ -449,7 +449,8 @@ def timeline_source(src):
     src = (src[:head.end() - 3] + ", unsigned long long* __restrict__ _ts) {\n"
            "  const unsigned long long _tsw_start = __builtin_amdgcn_s_memrealtime();" + src[head.end():])
     lines = src.split("\n")
-    first = next(i for i, ln in enumerate(lines) if "c_ptr" in ln and "store" in ln)
+    last_mfma = max(i for i, ln in enumerate(lines) if "newt::mfma" in ln)
+    first = next(i for i in range(last_mfma, len(lines)) if "c_ptr" in lines[i])
     while not (lines[first].startswith("  ") and not lines[first].startswith("   ")):
         first -= 1   # the top-level statement holding the first C store
     lines.insert(first, "  const unsigned long long _tsw_loop = __builtin_amdgcn_s_memrealtime();")
