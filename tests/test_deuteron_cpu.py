@@ -234,3 +234,33 @@ def test_untuned_kernel_uses_a_default_and_persists_nothing(tmp_path, monkeypatc
     cfg = SearchSpace(spec.traced).default()
     assert cfg["BLOCK_TILE_M"] == 256 and cfg.num_stages == 4
     assert not (tmp_path / "configs.json").exists()
+
+
+def test_tuner_confirms_its_fastest_candidates(monkeypatch):
+    """After its search, deuteron's tuner times its three fastest distinct
+    candidates again, back to back and twice over, and keeps the fastest of
+    those runs: a candidate timed on cold clocks during the search can still
+    win."""
+    from newt_amd import testing
+    from newt_amd.deuteron.runtime import Config, Tuner
+
+    cfgs = {n: Config({"BLOCK_TILE_M": n}) for n in (16, 32, 64, 128, 256)}
+    t = object.__new__(Tuner)
+    t.trials = [(cfgs[16], 3.0, ""), (cfgs[32], 1.0, ""), (cfgs[64], 2.0, ""),
+                (cfgs[128], None, "wrong result"), (cfgs[256], 4.0, ""), (cfgs[32], 1.5, "")]
+    launched = []
+
+    class Spec:
+        def launch(self, work, cfg):
+            launched.append(cfg["BLOCK_TILE_M"])
+    t.spec, t.work = Spec(), []
+    again = {16: [0.9, 0.7], 32: [1.1, 1.0], 64: [2.0, 1.9]}
+
+    def fake_bench(fn, warmup, rep):
+        fn()
+        n = launched[-1]
+        return again[n][sum(1 for x in launched if x == n) - 1]
+    monkeypatch.setattr(testing, "do_bench", fake_bench)
+    best, ms = t.confirm(cfgs[32], 1.0)
+    assert launched == [32, 64, 16, 32, 64, 16]    # the 3 fastest, two rounds
+    assert best["BLOCK_TILE_M"] == 16 and ms == 0.7
