@@ -29,6 +29,7 @@ import ast
 import builtins
 import math
 import os
+import re
 
 from . import layouts as lo
 from . import types as tp
@@ -776,16 +777,64 @@ class Codegen(ast.NodeVisitor):
             out.append(f"  __shared__ __attribute__((aligned(16))) unsigned char _lds[{lds_total}];")
         for nm, nb in self.lds_arrays:
             out.append(f"  __shared__ __attribute__((aligned(16))) unsigned char {nm}[{nb}];")
-        out.append("  const int _tid = (int)threadIdx.x;")
-        out.append("  const int _lane = _tid & 63;")
-        out.append("  const int _wave = __builtin_amdgcn_readfirstlane(_tid >> 6);")
-        out.append("  (void)_lane; (void)_wave;")
-        for p in self.prologue:
-            out.append("  " + p)
-        out += self.lines
+        body = ["  const int _tid = (int)threadIdx.x;",
+                "  const int _lane = _tid & 63;",
+                "  const int _wave = __builtin_amdgcn_readfirstlane(_tid >> 6);",
+                "  (void)_lane; (void)_wave;"]
+        body += ["  " + p for p in self.prologue]
+        out += self.version_body(body + self.lines)
         out.append("}")
         self.lds_total = lds_all
         return "\n".join(out) + "\n"
+
+    _CIDENT = re.compile(r"[A-Za-z_]\w*")
+    _BRANCH = re.compile(r"^\s*if \((.*)\) \{$")
+    # hipRTC's time grows faster than the body: a 4,700-line body took 4.7 s,
+    # its two copies 29.5 s
+    VERSION_MAX_LINES = 1200
+
+    def version_body(self, lines):
+        """Version a small, loop-free kernel body once on its uniform "tile in
+        bounds" test. Masked loads, stores and `where`s each branch on such a
+        test; when one test over scalar kernel arguments only guards two or
+        more of them, the whole body is emitted twice: `if (test) { body, test
+        folded to true } else { body }`. The first copy is straight-line code
+        the scheduler can order freely; the second is the body as generated.
+        Both compute the same values, so results are identical. The lane
+        index arithmetic of the prologue goes into both copies too (measured
+        1.5% faster than computing it once before the test). On layernorm
+        4096x8192: 20.9 against 23.1 us back to back, 28.1 against 29.0 us
+        flushed. Tests over per-program values (vector add's) are left
+        alone: versioning the body after the values they read measured 1.3%
+        slower. So are bodies with loops (the dot pipeline versions its own
+        loops) and bodies over VERSION_MAX_LINES. NEWT_VERSION_BODY=0 turns it
+        off."""
+        if os.environ.get("NEWT_VERSION_BODY", "1") == "0" or len(lines) > self.VERSION_MAX_LINES:
+            return lines
+        text = "\n".join(lines)
+        if re.search(r"\b(for|while|do|goto)\b", text):
+            return lines
+        params = {p.cname for _, p in self.params}
+        counts = {}
+        for ln in lines:
+            m = self._BRANCH.match(ln)
+            if m:
+                counts[m.group(1)] = counts.get(m.group(1), 0) + 1
+        for cond, n in sorted(counts.items(), key=lambda kv: -kv[1]):
+            if n < 2:
+                break
+            names = set(self._CIDENT.findall(cond)) - {"true", "false"}
+            if not names or not names <= params:
+                continue
+            # an argument the body assigns would not keep the test's value
+            if any(re.search(rf"\b{nm}\s*([-+*/%&|^]|<<|>>)?=(?!=)", text)
+                   or re.search(rf"(\+\+|--)\s*{nm}\b|\b{nm}\s*(\+\+|--)", text)
+                   for nm in names):
+                continue
+            fast = ["  " + ln.replace(cond, "(true)") for ln in lines]
+            slow = ["  " + ln for ln in lines]
+            return [f"  if ({cond}) {{"] + fast + ["  } else {"] + slow + ["  }"]
+        return lines
 
     # -------------------------------------------------------------- statements
     def visit_Expr(self, node):

@@ -609,7 +609,9 @@ LN_ARGS = {"x_ptr": (F16P, A16), "w_ptr": (F16P, A16), "b_ptr": (F16P, A16),
 def test_repeated_binop_is_computed_once(monkeypatch):
     """layernorm writes `x - mean` for the variance and again for the output:
     the second use takes the first block's registers (x - mean is evaluated
-    once per element), and NEWT_CSE=0 restores the recomputation."""
+    once per element), and NEWT_CSE=0 restores the recomputation (counted
+    in the body as generated, without the whole-body versioning copy)."""
+    monkeypatch.setenv("NEWT_VERSION_BODY", "0")
     sub = re.compile(r"= \(\(\(float\)\(_r\d+\[0\]\)\) - _t\d+\);")
     src, _ = compile_source(W.layernorm_kernel, LN_ARGS, {"BLOCK_N": 8192})
     assert len(sub.findall(src)) == 1
@@ -697,3 +699,52 @@ def test_bench_timeline_source_compiles():
     inst = bench.timeline_source(src)
     assert inst.count("s_memrealtime") == 3 and "_ts[_tsw_wg * 4 + 3]" in inst
     assert "s_memrealtime" in isa(inst)
+
+
+def test_whole_body_versioning(monkeypatch):
+    """A small loop-free kernel whose masked accesses share one uniform
+    in-bounds test over scalar arguments is emitted twice: `if (test) { body,
+    test folded to true } else { body }`. The fallback is the body as
+    generated; the fast copy keeps the masked branches only as dead code.
+    Tests over per-program values (vector add), bodies with loops, bodies over
+    the size limit and NEWT_VERSION_BODY=0 keep the single body."""
+    src, _ = compile_source(W.layernorm_kernel, LN_ARGS, {"BLOCK_N": 8192}, num_warps=8)
+    lines = src.split("\n")
+    # the first statement after the LDS declarations is the version test; the
+    # lane index arithmetic is inside both copies
+    i = next(i for i, ln in enumerate(lines) if re.match(r"^  if \(.*\) \{$", ln))
+    assert "__shared__" in lines[i - 1] and "_tid" in lines[i + 1]
+    cond = re.match(r"^  if \((.*)\) \{$", lines[i]).group(1)
+    j = lines.index("  } else {", i)
+    fast, slow = "\n".join(lines[i + 1:j]), "\n".join(lines[j + 1:])
+    assert set(re.findall(r"[A-Za-z_]\w*", cond)) == {"N"}
+    assert cond not in fast and fast.count("if ((true)) {") == slow.count(f"if ({cond})") >= 2
+    asm = isa(src)
+    assert "global_load_dwordx4" in asm and "global_store_dwordx4" in asm
+
+    monkeypatch.setenv("NEWT_VERSION_BODY", "0")
+    src0, _ = compile_source(W.layernorm_kernel, LN_ARGS, {"BLOCK_N": 8192}, num_warps=8)
+    assert "if ((true))" not in src0 and src0.count(f"if ({cond})") == slow.count(f"if ({cond})")
+    monkeypatch.delenv("NEWT_VERSION_BODY")
+
+    # the add kernel's test is over the program's first element: one body
+    assert "if ((true))" not in compile_source(W.add_kernel, ADD_ARGS, {"BLOCK": 1024})[0]
+
+    # a loop in the body: one body
+    def k(x_ptr, o_ptr, n, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        acc = nl.zeros((BLOCK,), dtype=nl.float32)
+        for i in range(0, 4):
+            acc += nl.load(x_ptr + i * n + offs, mask=offs < n, other=0.0)
+        nl.store(o_ptr + offs, acc, mask=offs < n)
+    args = {"x_ptr": (F32P, A16), "o_ptr": (F32P, A16), "n": tp.int32}
+    assert "if ((true))" not in compile_source(k, args, {"BLOCK": 256})[0]
+
+    # a body over the size limit: one body
+    def big(x_ptr, o_ptr, n, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        x = nl.load(x_ptr + offs, mask=offs < n, other=0.0)
+        nl.store(o_ptr + offs, x * 2.0, mask=offs < n)
+    small_src = compile_source(big, args, {"BLOCK": 1024})[0]
+    assert "if ((true))" in small_src
+    assert "if ((true))" not in compile_source(big, args, {"BLOCK": 1 << 16}, num_warps=1)[0]
