@@ -831,7 +831,11 @@ class Codegen(ast.NodeVisitor):
                    or re.search(rf"(\+\+|--)\s*{nm}\b|\b{nm}\s*(\+\+|--)", text)
                    for nm in names):
                 continue
-            fast = ["  " + ln.replace(cond, "(true)") for ln in lines]
+            # only whole `if (test) {` lines are rewritten: the test's text may
+            # also occur inside a longer expression that means something else
+            branch = f"if ({cond}) {{"
+            fast = ["  " + (ln.replace(branch, "if ((true)) {") if self._BRANCH.match(ln) else ln)
+                    for ln in lines]
             slow = ["  " + ln for ln in lines]
             return [f"  if ({cond}) {{"] + fast + ["  } else {"] + slow + ["  }"]
         return lines

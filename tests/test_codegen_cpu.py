@@ -748,3 +748,33 @@ def test_whole_body_versioning(monkeypatch):
     small_src = compile_source(big, args, {"BLOCK": 1024})[0]
     assert "if ((true))" in small_src
     assert "if ((true))" not in compile_source(big, args, {"BLOCK": 1 << 16}, num_warps=1)[0]
+
+
+def test_whole_body_versioning_leaves_runtime_ifs_alone():
+    """A runtime `if` on a scalar argument evaluates its test into a per-program
+    temporary first, so repeated user tests are not taken for the in-bounds test
+    and the body stays single; the masked accesses' own test still versions it,
+    and the user's tests keep their text in both copies."""
+    def k(x_ptr, o_ptr, m, n, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        x = nl.load(x_ptr + offs)
+        if n > 0:
+            x = x + 1.0
+        if n > 0:
+            x = x * 2.0
+        nl.store(o_ptr + offs, x + (m + n > 0))
+    args = {"x_ptr": (F32P, A16), "o_ptr": (F32P, A16), "m": tp.int32, "n": tp.int32}
+    src = compile_source(k, args, {"BLOCK": 256})[0]
+    assert "if ((true))" not in src and src.count("(n > 0)") == 2
+    isa(src)
+
+    def km(x_ptr, o_ptr, n, BLOCK: nl.constexpr):
+        offs = nl.arange(0, BLOCK)
+        x = nl.load(x_ptr + offs, mask=offs < n, other=0.0)
+        if n > 8:
+            x = x + 1.0
+        nl.store(o_ptr + offs, x, mask=offs < n)
+    args = {"x_ptr": (F32P, A16), "o_ptr": (F32P, A16), "n": tp.int32}
+    src = compile_source(km, args, {"BLOCK": 256})[0]
+    assert src.count("if ((true)) {") == 2 and src.count("(n > 8)") == 2
+    isa(src)
