@@ -13,6 +13,11 @@ samples it so that every program of the launch is touched:
              the last row, against all N columns: relative Frobenius error
              <= 1e-2 (north_star) and every sampled element within one ulp of
              the fp64 product rounded to the output dtype.
+  softmax    fp32 [4096, C] for C in {1000, 4096, 8192} and layernorm fp16
+             [4096, 8192] (examples/02 and 03 at the benchmark shapes, both
+             paths of their in-bounds test: 1000 < BLOCK_N takes the masked
+             body, 4096 and 8192 the straight-line one): every row against the
+             oracle, at the tolerances of the small-shape tests.
   attention  (the default kernel and the examples/05 plain form)
              eight (batch, head) pairs spread over all 128, with the query
              rows of the first, a middle and the last 128-row query block:
@@ -92,3 +97,24 @@ def test_attention_benchmark_shape(W, causal, plain):
         assert err <= 1e-2, f"(b={bi}, h={hi}) rel_frobenius {err}"
         assert row_err <= 1e-2, f"(b={bi}, h={hi}) worst row rel_frobenius {row_err}"
     print(f"  worst per-row rel_frobenius {worst:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("C", [1000, 4096, 8192])
+def test_softmax_benchmark_shapes(W, C):
+    print(f"softmax fp32 [4096, {C}]", flush=True)
+    x = seeded((4096, C), 0, scale=4.0)
+    out = W.softmax(x)
+    np.testing.assert_allclose(npf(out), orc.softmax_rows(npf(x)), rtol=1e-5, atol=1e-6)
+
+
+def test_layernorm_benchmark_shape(W):
+    print("layernorm fp16 [4096, 8192]", flush=True)
+    M, N = 4096, 8192
+    x = seeded((M, N), 0, dtype=torch.float16)
+    w = (seeded((N,), 2, scale=0.1) + 1.0).half()
+    b = seeded((N,), 3, scale=0.1, dtype=torch.float16)
+    y, mean, rstd = W.layernorm(x, w, b, 1e-5)
+    ry, rmean, rrstd = orc.layernorm_rows(npf(x), npf(w), npf(b), 1e-5, "float16")
+    np.testing.assert_allclose(npf(y), ry, rtol=2e-3, atol=2e-3)
+    np.testing.assert_allclose(npf(mean), rmean, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(npf(rstd), rrstd, rtol=1e-5, atol=1e-6)
