@@ -140,13 +140,112 @@ def ulp_violations(actual, expected, dtype, atol=1e-6):
     return int(np.count_nonzero(bad | np.isnan(a)))
 
 
-def panel_rows(M, block=64, extra=(0,)):
+U_FP32 = 2.0 ** -24     # unit roundoff of fp32 (half its relative ulp)
+U_FP16_SUB = 2.0 ** -24  # spacing of fp16 subnormals
+
+
+def rel_violations(actual, expected, rtol, floor=1e-30):
+    """Number of elements farther than rtol * |expected| + floor from
+    `expected` (NaN counts as a violation). A relative check: the floor
+    only keeps an exact zero of the oracle from demanding an exact zero of
+    the kernel, so a kernel that writes 0 where the oracle holds a small
+    positive value fails."""
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    ok = np.abs(a - e) <= rtol * np.abs(e) + floor
+    return int(np.count_nonzero(~ok))
+
+
+def mean_violations(actual, expected, x, rtol=1e-5):
+    """Rows whose fp32 mean is farther than rtol * |mean| + U_FP32 * mean(|x|)
+    from the exact one.
+
+    A mean is an fp32 sum of the N terms of a row: its rounding error in any
+    reduction tree of depth D is at most about D * U_FP32 * sum(|x_i|)
+    (Higham, Accuracy and Stability of Numerical Algorithms, 2nd ed., 4.2),
+    which rtol * |mean| cannot hold where the row's sum cancels. The floor
+    U_FP32 * mean(|x|) is 1/D of that worst case (D ~ 30 for 8192 terms: 16
+    per thread, 6 lane levels, 8 waves) and ~13x the largest error of fp32
+    tree sums over the benchmark rows (N(0,1), N = 8192); it is far below
+    the shift of a planted mistake such as dividing by N - 1 (|mean| / N)."""
+    a = np.asarray(actual, np.float64).reshape(-1)
+    e = np.asarray(expected, np.float64).reshape(-1)
+    xs = np.abs(np.asarray(x, np.float64)).mean(axis=1)
+    ok = np.abs(a - e) <= rtol * np.abs(e) + U_FP32 * xs
+    return int(np.count_nonzero(~ok))
+
+
+def layernorm_violations(y, mean, rstd, x, w, b, eps=1e-5, out_dtype="float16", rtol=1e-5):
+    """Element / row counts of a layernorm result beyond its tolerance, per
+    output, against layernorm_rows on the same inputs:
+      y     fp16 / bf16 output: within one ulp of the exact result rounded to
+            the output dtype (ulp_violations; the absolute slack is the fp16
+            subnormal spacing 2^-24, or 0 for bf16); fp32 output: within rtol
+            of the magnitude of the terms, rtol * (|x - mean| * rstd * |w| + |b|),
+            since y itself cancels where b meets the normalised term
+      mean  mean_violations (rtol, floor one fp32 unit of mean(|x|))
+      rstd  rtol, relative (a sum of squares does not cancel)"""
+    ry, rm, rr = layernorm_rows(x, w, b, eps, out_dtype)
+    if out_dtype in ("float16", "bfloat16"):
+        y_bad = ulp_violations(y, ry, out_dtype,
+                               atol=U_FP16_SUB if out_dtype == "float16" else 0.0)
+    else:
+        xf = np.asarray(x, np.float64)
+        scale = (np.abs(xf - rm.astype(np.float64)[:, None]) * rr.astype(np.float64)[:, None]
+                 * np.abs(np.asarray(w, np.float64))[None, :]
+                 + np.abs(np.asarray(b, np.float64))[None, :])
+        d = np.abs(np.asarray(y, np.float64) - ry)
+        y_bad = int(np.count_nonzero(~(d <= rtol * scale)))
+    return {"y": y_bad, "mean": mean_violations(mean, rm, x, rtol),
+            "rstd": rel_violations(rstd, rr, rtol)}
+
+
+def panel_rows(M, block=64, extra=(0,), shift=0):
     """Row indices touching every `block`-row panel of an M-row output (one
     row per panel at an offset that cycles through the panel, so different
-    waves and lanes are sampled), plus M - 1 and `extra`."""
-    rows = {p * block + (p * 29 + 7) % block for p in range((M + block - 1) // block)}
+    waves and lanes are sampled; `shift` moves every offset, so calls for
+    different heads or batches sample different lanes), plus M - 1 and
+    `extra`."""
+    rows = {p * block + (p * 29 + 7 + shift) % block for p in range((M + block - 1) // block)}
     rows = {r for r in rows if r < M} | {M - 1} | {r for r in extra if 0 <= r < M}
     return np.array(sorted(rows))
+
+
+def attention_sampled_errors(q, k, v, o, scale, causal, block=128, dense_pairs=8,
+                             p_dtype="bfloat16", out_dtype="bfloat16"):
+    """Relative Frobenius errors of an attention output o [B, H, S, D] against
+    `attention` on rows that touch every program of a launch whose programs
+    own `block` query rows (or a multiple of them) of one (batch, head):
+      sampled  every (batch, head) pair, one row of every `block`-row query
+               block, at an offset that cycles through the block and moves
+               with the pair (panel_rows with a per-pair shift)
+      dense    `dense_pairs` pairs spread over all of them, every row of the
+               first, a middle and the last query block
+    Returns {"rows": rows checked, "worst_row": the largest per-row error,
+    "worst_pair": the largest error over one pair's dense rows}."""
+    B, H, S, D = q.shape
+    nb = (S + block - 1) // block
+    dense = np.concatenate([np.arange(i * block, min(S, (i + 1) * block))
+                            for i in sorted({0, nb // 2, nb - 1})])
+    dense_set = set(int(i) for i in spread(B * H, dense_pairs))
+    worst_row, worst_pair, count = 0.0, 0.0, 0
+    for bh in range(B * H):
+        bi, hi = divmod(bh, H)
+        rows = panel_rows(S, block, extra=(), shift=bh * 13)
+        if bh in dense_set:
+            rows = np.union1d(rows, dense)
+        ref = attention(q[bi, hi, rows], k[bi, hi], v[bi, hi], scale, causal, p_dtype=p_dtype,
+                        out_dtype=out_dtype, q_pos=rows)
+        got = o[bi, hi, rows]
+        num = np.linalg.norm(got.astype(np.float64) - ref, axis=1)
+        den = np.maximum(np.linalg.norm(ref.astype(np.float64), axis=1), 1e-30)
+        bad = np.isnan(got).any(axis=1)
+        worst_row = max(worst_row, float(np.max(np.where(bad, np.inf, num / den))))
+        if bh in dense_set:
+            sel = np.isin(rows, dense)
+            worst_pair = max(worst_pair, rel_frobenius(got[sel], ref[sel]))
+        count += len(rows)
+    return {"rows": count, "worst_row": worst_row, "worst_pair": worst_pair}
 
 
 def spread(n, count):

@@ -17,11 +17,20 @@ samples it so that every program of the launch is touched:
              [4096, 8192] (examples/02 and 03 at the benchmark shapes, both
              paths of their in-bounds test: 1000 < BLOCK_N takes the masked
              body, 4096 and 8192 the straight-line one): every row against the
-             oracle, at the tolerances of the small-shape tests.
-  attention  (the default kernel and the examples/05 plain form)
-             eight (batch, head) pairs spread over all 128, with the query
-             rows of the first, a middle and the last 128-row query block:
-             relative Frobenius error <= 1e-2 per (batch, head) and per row.
+             oracle, at the tolerances of the small-shape tests: softmax
+             rtol 1e-5 on every element (relative, no absolute floor
+             beyond 1e-30); layernorm y within one fp16 ulp of the exact
+             result rounded to fp16, mean rtol 1e-5 with a floor of one
+             fp32 unit of mean(|x|) for rows whose sum cancels, rstd rtol
+             1e-5 (oracle.layernorm_violations).
+  attention  (the default kernel and the examples/05 plain form) every
+             (batch, head) pair, one query row of every 128-row block (the
+             causal launch's programs; the non-causal ones own two such
+             blocks) at an offset that cycles through the block and moves
+             with the pair, plus every row of the first, a middle and the
+             last block of eight pairs spread over all 128: relative
+             Frobenius error <= 1e-2 per row and per pair
+             (oracle.attention_sampled_errors).
 """
 
 import numpy as np
@@ -70,7 +79,7 @@ def test_matmul_square_autotuned(W, S, dtype):
     assert bad == 0, f"{bad} of {got.size} sampled elements beyond one ulp"
 
 
-QUERY_BLOCK = 128
+QUERY_BLOCK = 128   # the smaller of the two query-block sizes launched (128 causal, 256 not)
 
 
 @pytest.mark.parametrize("plain", [False, True], ids=["default", "plain_form"])
@@ -81,22 +90,14 @@ def test_attention_benchmark_shape(W, causal, plain):
     q, k, v = (seeded((B, H, S, D), s, dtype=torch.bfloat16) for s in (6, 7, 8))
     o = W.attention(q, k, v, causal=causal, plain=plain)
     torch.cuda.synchronize()
-    blocks = S // QUERY_BLOCK
-    rows = np.concatenate([np.arange(i * QUERY_BLOCK, (i + 1) * QUERY_BLOCK)
-                           for i in (0, blocks // 2, blocks - 1)])
-    rows_t = torch.from_numpy(rows).cuda()
-    worst = 0.0
-    for bh in orc.spread(B * H, 8):
-        bi, hi = divmod(int(bh), H)
-        ref = orc.attention(npf(q[bi, hi, rows_t]), npf(k[bi, hi]), npf(v[bi, hi]), D ** -0.5,
-                            causal, p_dtype="bfloat16", out_dtype="bfloat16", q_pos=rows)
-        got = npf(o[bi, hi, rows_t])
-        err = orc.rel_frobenius(got, ref)
-        row_err = max(orc.rel_frobenius(got[r], ref[r]) for r in range(len(rows)))
-        worst = max(worst, row_err)
-        assert err <= 1e-2, f"(b={bi}, h={hi}) rel_frobenius {err}"
-        assert row_err <= 1e-2, f"(b={bi}, h={hi}) worst row rel_frobenius {row_err}"
-    print(f"  worst per-row rel_frobenius {worst:.3e}", flush=True)
+    # every program: one row of every 128-row query block of every (batch,
+    # head) pair, plus every row of three blocks of eight pairs
+    res = orc.attention_sampled_errors(npf(q), npf(k), npf(v), npf(o), D ** -0.5, causal,
+                                       block=QUERY_BLOCK)
+    print(f"  {res}", flush=True)
+    assert res["rows"] >= B * H * (S // QUERY_BLOCK)
+    assert res["worst_row"] <= 1e-2, res
+    assert res["worst_pair"] <= 1e-2, res
 
 
 @pytest.mark.parametrize("C", [1000, 4096, 8192])
@@ -104,7 +105,11 @@ def test_softmax_benchmark_shapes(W, C):
     print(f"softmax fp32 [4096, {C}]", flush=True)
     x = seeded((4096, C), 0, scale=4.0)
     out = W.softmax(x)
-    np.testing.assert_allclose(npf(out), orc.softmax_rows(npf(x)), rtol=1e-5, atol=1e-6)
+    got, ref = npf(out), orc.softmax_rows(npf(x))
+    bad = orc.rel_violations(got, ref, 1e-5)
+    rel = float(np.max(np.abs(got.astype(np.float64) - ref) / np.maximum(ref, 1e-30)))
+    print(f"  max relative error {rel:.3e}, smallest probability {ref.min():.3e}", flush=True)
+    assert bad == 0, f"{bad} of {got.size} elements beyond rtol 1e-5 (max {rel:.3e})"
 
 
 def test_layernorm_benchmark_shape(W):
@@ -114,7 +119,7 @@ def test_layernorm_benchmark_shape(W):
     w = (seeded((N,), 2, scale=0.1) + 1.0).half()
     b = seeded((N,), 3, scale=0.1, dtype=torch.float16)
     y, mean, rstd = W.layernorm(x, w, b, 1e-5)
-    ry, rmean, rrstd = orc.layernorm_rows(npf(x), npf(w), npf(b), 1e-5, "float16")
-    np.testing.assert_allclose(npf(y), ry, rtol=2e-3, atol=2e-3)
-    np.testing.assert_allclose(npf(mean), rmean, rtol=1e-5, atol=1e-6)
-    np.testing.assert_allclose(npf(rstd), rrstd, rtol=1e-5, atol=1e-6)
+    bad = orc.layernorm_violations(npf(y), npf(mean), npf(rstd), npf(x), npf(w), npf(b), 1e-5,
+                                   "float16")
+    print(f"  violations {bad}", flush=True)
+    assert bad == {"y": 0, "mean": 0, "rstd": 0}

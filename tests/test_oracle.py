@@ -280,3 +280,110 @@ def test_panel_rows_cover_every_panel():
             assert len(set(rows % block)) > 4
     s = orc.spread(128, 8)
     assert s[0] == 0 and s[-1] == 127 and len(s) == 8
+
+
+# ---------------------------------------------------------------- tolerance checkers
+
+def _bench_like_rows(M, N, seed=0):
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((M, N)).astype(np.float16).astype(np.float32)
+
+
+def _fp32_layernorm(x, w, b, eps, unbiased=False, mean_div=None):
+    """A plain fp32 evaluation of examples/03 in a reduction order like a
+    GPU's (16 terms per thread, then a tree): what a correct kernel does."""
+    M, N = x.shape
+    x = x.astype(np.float32)
+    part = x.reshape(M, -1, N // 16 if N % 16 == 0 else N).sum(axis=1, dtype=np.float32)
+    mean = (part.sum(axis=1, dtype=np.float32) / np.float32(mean_div or N)).astype(np.float32)
+    d = (x - mean[:, None]).astype(np.float32)
+    sq = (d * d).astype(np.float32).reshape(part.shape[0], -1, part.shape[1])
+    var = (sq.sum(axis=1, dtype=np.float32).sum(axis=1, dtype=np.float32)
+           / np.float32(N - 1 if unbiased else N)).astype(np.float32)
+    rstd = (np.float32(1) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    y = (d * rstd[:, None]).astype(np.float32) * w.astype(np.float32)[None, :] + b.astype(np.float32)
+    return y.astype(np.float32), mean, rstd
+
+
+def test_rel_violations():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 4096)) * 4).astype(np.float32)
+    ref = orc.softmax_rows(x)
+    # an fp32 evaluation (exp, sum and divide in fp32) is within rtol 1e-5
+    e = np.exp(x - x.max(axis=1, keepdims=True)).astype(np.float32)
+    fp32 = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    assert orc.rel_violations(fp32, ref, 1e-5) == 0
+    assert orc.rel_violations(ref * (1 + 0.9e-5), ref, 1e-5) == 0
+    # zeroing the probabilities under 1e-6 (which an atol of 1e-6 would pass)
+    small = np.where(ref < 1e-6, 0.0, ref)
+    assert orc.rel_violations(small, ref, 1e-5) > ref.size // 4
+    # a mid-range probability 1e-4 off, an exp with a 2e-5 relative error, a NaN
+    bad = ref.copy()
+    mid = np.argwhere((ref > 1e-5) & (ref < 1e-3))[0]
+    bad[tuple(mid)] *= 1 + 1e-4
+    assert orc.rel_violations(bad, ref, 1e-5) == 1
+    assert orc.rel_violations(ref * (1 + 2e-5), ref, 1e-5) == ref.size
+    bad[-1, -1] = np.nan
+    assert tuple(mid) != (63, 4095) and orc.rel_violations(bad, ref, 1e-5) == 2
+    # exact zeros of the oracle: an exact zero passes, a nonzero value fails
+    assert orc.rel_violations(np.array([0.0, 1e-31]), np.array([0.0, 0.0]), 1e-5) == 0
+    assert orc.rel_violations(np.array([1e-20]), np.array([0.0]), 1e-5) == 1
+
+
+def test_layernorm_violations_accept_fp32_and_reject_mistakes():
+    M, N = 256, 8192
+    x = _bench_like_rows(M, N)
+    rng = np.random.default_rng(5)
+    w = (1 + 0.1 * rng.standard_normal(N)).astype(np.float16).astype(np.float32)
+    b = (0.1 * rng.standard_normal(N)).astype(np.float16).astype(np.float32)
+    y, mean, rstd = _fp32_layernorm(x, w, b, 1e-5)
+    for dt in ("float16", "float32"):
+        got = orc.round_to(y, dt)
+        assert orc.layernorm_violations(got, mean, rstd, x, w, b, 1e-5, dt) == \
+            {"y": 0, "mean": 0, "rstd": 0}
+    # the mean divided by N - 1, the unbiased variance, a dropped element
+    _, m1, _ = _fp32_layernorm(x, w, b, 1e-5, mean_div=N - 1)
+    assert orc.mean_violations(m1, orc.layernorm_rows(x, w, b)[1], x) > M // 2
+    _, _, r1 = _fp32_layernorm(x, w, b, 1e-5, unbiased=True)
+    assert orc.layernorm_violations(orc.round_to(y, "float16"), mean, r1, x, w, b, 1e-5,
+                                    "float16")["rstd"] == M
+    x2 = x.copy()
+    x2[:, -1] = 0.0
+    _, m2, _ = _fp32_layernorm(x2, w, b, 1e-5)
+    assert orc.mean_violations(m2, orc.layernorm_rows(x, w, b)[1], x) > M // 2
+    # y two fp16 ulps off, one element's sign flipped
+    y16 = orc.round_to(y, "float16")
+    off = y16 + np.abs(y16) * 2.0 ** -9
+    assert orc.layernorm_violations(off, mean, rstd, x, w, b, 1e-5, "float16")["y"] > y.size // 2
+    flip = y16.copy()
+    flip[3, 5] = -flip[3, 5] if abs(flip[3, 5]) > 1e-3 else 1.0
+    assert orc.layernorm_violations(flip, mean, rstd, x, w, b, 1e-5, "float16")["y"] == 1
+    # fp32 output: the same planted offsets fail the term-scaled rtol
+    assert orc.layernorm_violations(y * (1 + 1e-4), mean, rstd, x, w, b, 1e-5,
+                                    "float32")["y"] > y.size // 2
+
+
+def test_attention_sampled_errors_touch_every_program():
+    """The sampled attention check passes the oracle's own output and fails
+    when any one program's rows are wrong (each (batch, head) x query block
+    in turn, on a small launch shaped like the benchmark's)."""
+    rng = np.random.default_rng(9)
+    B, H, S, D, block = 1, 3, 96, 16, 32
+    q, k, v = (orc.round_bf16(rng.standard_normal((B, H, S, D)).astype(np.float32))
+               for _ in range(3))
+    for causal in (False, True):
+        o = orc.attention(q, k, v, D ** -0.5, causal, p_dtype="bfloat16", out_dtype="bfloat16")
+        ok = orc.attention_sampled_errors(q, k, v, o, D ** -0.5, causal, block=block,
+                                          dense_pairs=2)
+        assert ok["worst_row"] < 1e-6 and ok["worst_pair"] < 1e-6
+        assert ok["rows"] >= B * H * (S // block)
+        for bh in range(B * H):
+            for blk in range(S // block):
+                bad = o.copy()
+                bi, hi = divmod(bh, H)
+                # the program's rows taken from another head: plausible values, wrong ones
+                bad[bi, hi, blk * block:(blk + 1) * block] = \
+                    o[bi, (hi + 1) % H, blk * block:(blk + 1) * block]
+                res = orc.attention_sampled_errors(q, k, v, bad, D ** -0.5, causal, block=block,
+                                                   dense_pairs=2)
+                assert res["worst_row"] > 1e-2, (causal, bh, blk)
