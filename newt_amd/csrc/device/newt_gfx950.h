@@ -4,8 +4,9 @@
 // as an in-memory include). Generated code keeps the per-element arithmetic; the
 // hardware-specific pieces live here:
 //   * 16-byte vector global loads/stores (global_load_dwordx4 / store_dwordx4)
-//   * wave64 cross-lane butterflies on DPP (quad_perm) and ds_swizzle, with a
-//     ds_bpermute fallback only for the xor-32 step across the two wave halves
+//   * wave64 cross-lane butterflies on the VALU: DPP (quad_perm, row mirrors)
+//     and v_permlane16/32_swap; ds_swizzle / ds_bpermute only for partial
+//     lane masks
 //   * MFMA wrappers for the fp16/bf16/fp32 matrix-core instructions of CDNA4
 //   * XOR-swizzled LDS tile addressing for MFMA operand staging
 //   * float atomic max as a CAS loop on vector memory
@@ -44,8 +45,11 @@ __device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
 // exp on the transcendental unit: exp(x) = exp2(x * log2 e) with one rounding
 // of the product, then v_exp_f32 (1 ulp). Relative error <= |x| * 1.5 * 2^-24
 // + 2^-23, under 8e-6 for every x whose result is a normal float (|x| < 88),
-// against ~13 instructions for the library's range-reduced form. Results below
-// 2^-126 flush to zero; +-inf and NaN propagate.
+// against ~13 instructions for the library's range-reduced form. +-inf and
+// NaN propagate. Two deviations from expf: results below 2^-126 (x < -87.34)
+// flush to zero where expf returns a subnormal, and an x within an ulp below
+// ln(FLT_MAX) whose product with log2 e rounds to 128.0 gives inf where expf
+// gives ~3.4e38.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float exp_f32(float x) {
   return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);

@@ -165,7 +165,9 @@ class SearchSpace:
         footprint = self.span_elements
         for name in self.tiles:
             footprint *= cfg[name]
-        return footprint <= _ELT_FOOTPRINT
+        # a whole-dimension span wider than the cap still gets the smallest
+        # footprint there is (every tile 1), with each num_warps
+        return footprint <= max(_ELT_FOOTPRINT, self.span_elements)
 
     def every(self):
         names = list(self.values)
@@ -294,6 +296,9 @@ class Tuner:
 
         every = space.every()
         sample = every if len(every) <= samples else random.Random(0).sample(every, samples)
+        if not space.seeds() and not sample:
+            raise RuntimeError(f"deuteron: no candidate configuration for "
+                               f"{self.kernel.__name__} (empty search space)")
         best, best_ms = None, float("inf")
         for cfg in space.seeds() + sample:
             ms = run(cfg)

@@ -153,8 +153,9 @@ class Fill(Node):
 
 
 class Dot(Node):
-    def __init__(self, a, b, acc, mask_a):
-        self.a, self.b, self.acc, self.mask_a = a, b, acc, mask_a
+    def __init__(self, a, b, acc, mask_a, mask_b):
+        self.a, self.b, self.acc = a, b, acc
+        self.mask_a, self.mask_b = mask_a, mask_b
         self.axes = (a.axes[0], b.axes[1])
         pad = {d for d in a.live_padded() if d is a.axes[0].find()}
         pad |= {d for d in b.live_padded() if d is b.axes[1].find()}
@@ -429,11 +430,15 @@ class _Tracer:
             self.fail(node, "@ contracts two 2D tiles")
         _merge(a.axes[1], b.axes[0], node, self)
         k = a.axes[1].find() if a.axes[1] is not None else None
-        safe = lambda v: v.zero_padded or k not in v.live_padded()
+        # an operand whose padded k lanes may hold anything (a computed value:
+        # exp, log, a reciprocal of the zero a load put there) is zeroed there,
+        # whatever the other operand holds: 0 * inf is NaN, so a zero-padded
+        # load on the other side does not make the product safe
+        unsafe = lambda v: k is not None and not v.zero_padded and k in v.live_padded()
         self.has_dot = True
         if acc is not None:
             _broadcast([(a.axes[0], b.axes[1]), acc.axes], node, self)
-        return Dot(a, b, acc, mask_a=k is not None and not (safe(a) or safe(b)))
+        return Dot(a, b, acc, mask_a=unsafe(a), mask_b=unsafe(b))
 
     def expr(self, node):
         if isinstance(node, ast.Constant):
@@ -633,6 +638,9 @@ class _Renderer:
             if n.mask_a:
                 k = n.a.axes[1].find()
                 a = self.temp(depth, f"nl.where({_mask_text([k], n.a.axes)}, {a}, 0.0)")
+            if n.mask_b:
+                k = n.b.axes[0].find()
+                b = self.temp(depth, f"nl.where({_mask_text([k], n.b.axes)}, {b}, 0.0)")
             if n.acc is None:
                 return f"nl.dot({a}, {b})"
             return f"nl.dot({a}, {b}, {self.expr(n.acc, depth)})"

@@ -80,6 +80,35 @@ def test_dot_kernels_try_gfx950_seeds_first():
     assert sm.admits(sm.default())
 
 
+def test_a_span_wider_than_the_footprint_cap_keeps_its_smallest_tiles():
+    """A whole-dimension span above the cap (a 65536-wide row) still has
+    candidates: one row per program with each num_warps, and moves among
+    them; the search does not start from an empty space."""
+    from newt_amd.deuteron.runtime import SearchSpace
+    xs = torch.empty(8, 65536)
+    sm = SearchSpace(softmax._specialize((xs, xs)).traced, span_elements=65536)
+    every = sm.every()
+    assert every and all(c["BLOCK_TILE_M"] == 1 for c in every)
+    assert sorted(c.num_warps for c in every) == [1, 2, 4, 8]
+    assert sm.admits(sm.default()) and sm.default()["BLOCK_TILE_M"] == 1
+    assert sm.moves(every[0])
+
+
+def test_an_empty_search_space_is_its_own_error():
+    from newt_amd.deuteron.runtime import Tuner
+
+    class Empty:
+        def every(self):
+            return []
+
+        def seeds(self):
+            return []
+    t = object.__new__(Tuner)
+    t.kernel = softmax
+    with pytest.raises(RuntimeError, match="no candidate configuration"):
+        t.search(Empty(), 8)
+
+
 def test_masks_reach_reductions():
     x = torch.empty(10, 30)
     src = softmax.to_newt_source(x, x)
@@ -120,7 +149,7 @@ def test_mean_divides_by_the_true_extent():
     assert "(nl.sum(nl.where(x_all1_in[None, :], _t1, 0.0), axis=1) / (x_d1))" in src
 
 
-def test_dot_masks_an_operand_when_neither_is_zero_padded():
+def test_dot_masks_every_computed_operand_over_a_padded_k():
     @dt.kernel
     def expdot(x, y, out):
         for tm, tn in dt.tile([x.shape[0], y.shape[1]]):
@@ -136,11 +165,25 @@ def test_dot_masks_an_operand_when_neither_is_zero_padded():
             for tk in dt.tile(x.shape[1]):
                 acc += dt.exp(x[tm, tk]) @ y[tk, tn]
             out[tm, tn] = acc
+    @dt.kernel
+    def loaddot(x, y, out):
+        for tm, tn in dt.tile([x.shape[0], y.shape[1]]):
+            acc = dt.zeros([tm, tn], dtype=dt.float32)
+            for tk in dt.tile(x.shape[1]):
+                acc += x[tm, tk] @ dt.log(y[tk, tn])
+            out[tm, tn] = acc
     x, y, o = torch.empty(64, 32), torch.empty(32, 48), torch.empty(64, 48)
     src = expdot.to_newt_source(x, y, o)
     assert "nl.where(tk_in[None, :], nl.exp(_t1), 0.0)" in src
-    # one raw load (zero in its padded lanes) is enough
-    assert "nl.where(" not in halfexp.to_newt_source(x, y, o)
+    assert "nl.where(tk_in[:, None], nl.exp(_t2), 0.0)" in src
+    # a raw load on the other side is not enough: 0 * inf is NaN, so the
+    # computed operand is zeroed in its padded k lanes all the same
+    src = halfexp.to_newt_source(x, y, o)
+    assert "nl.where(tk_in[None, :], nl.exp(_t1), 0.0)" in src and src.count("nl.where(") == 1
+    src = loaddot.to_newt_source(x, y, o)
+    assert "nl.where(tk_in[:, None], nl.log(_t2), 0.0)" in src and src.count("nl.where(") == 1
+    # two raw loads (the matmul) need no mask
+    assert "nl.where(" not in matmul.to_newt_source(x.half(), y.half(), o.half())
 
 
 def _compile(tr, types, constexprs, num_warps=4, num_stages=2):

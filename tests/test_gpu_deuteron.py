@@ -193,11 +193,34 @@ def exp_dot(x, y, out):
 
 
 def test_dot_of_computed_tiles_over_a_ragged_k():
-    """exp(0) = 1 in both operands' padded k lanes: the tracer zeroes one
-    operand there, so K = 100 (not a multiple of 32) matches torch."""
+    """exp(0) = 1 in both operands' padded k lanes: the tracer zeroes each
+    computed operand there, so K = 100 (not a multiple of 32) matches torch."""
     x = torch.randn(128, 100, device="cuda", generator=_g(18)) * 0.1
     y = torch.randn(100, 96, device="cuda", generator=_g(19)) * 0.1
     out = torch.empty(128, 96, device="cuda")
     exp_dot(x, y, out)
     ref = x.exp().double() @ y.exp().double()
+    assert ((out.double() - ref).norm() / ref.norm()).item() < 1e-5
+
+
+@dt.kernel(config={"BLOCK_TM": 64, "BLOCK_TN": 64, "BLOCK_TK": 32, "num_warps": 4,
+                   "num_stages": 2})
+def log_dot(x, y, out):
+    for tm, tn in dt.tile([x.shape[0], y.shape[1]]):
+        acc = dt.zeros([tm, tn], dtype=dt.float32)
+        for tk in dt.tile(x.shape[1]):
+            acc += dt.log(x[tm, tk]) @ y[tk, tn]
+        out[tm, tn] = acc
+
+
+def test_dot_of_a_non_finite_padding_and_a_load_over_a_ragged_k():
+    """log(0) = -inf in the computed operand's padded k lanes and 0 in the
+    loaded operand's: -inf * 0 is NaN, so the tracer zeroes the computed
+    operand even though the other one is a zero-padded load (K = 100)."""
+    x = torch.rand(128, 100, device="cuda", generator=_g(20)) + 0.5
+    y = torch.randn(100, 96, device="cuda", generator=_g(21)) * 0.1
+    out = torch.empty(128, 96, device="cuda")
+    log_dot(x, y, out)
+    ref = x.log().double() @ y.double()
+    assert not out.isnan().any()
     assert ((out.double() - ref).norm() / ref.norm()).item() < 1e-5
