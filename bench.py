@@ -454,7 +454,9 @@ def _short_name(workload):
                         ("attention bf16 [4,32,4096,128] ", "attention "),
                         (" (examples/05 plain form)", " plain"),
                         (" (fp32 MFMA, full precision; the reference runs tf32)", ""),
-                        (" (autotuned tile DSL)", ""), ("fp32 ", ""), ("fp16 ", "")):
+                        (" (autotuned tile DSL)", ""), ("fp32 ", ""), ("fp16 ", ""),
+                        ("host launch cost: add n=1e6 via @newt.jit (value) and torch.add(out=)",
+                         "host launch (newt add)")):
         w = w.replace(long, short)
     if workload.startswith("matmul"):
         w = workload.split(" (")[0]
@@ -687,6 +689,34 @@ def warm_up(fn, seconds=0.2):
     settle_clocks(fn, seconds)
 
 
+def host_launch_cost(launches=1000):
+    """Host time per launch of the vector add (n = 10^6) through @newt.jit,
+    and of torch.add(x, y, out=o) for comparison: `launches` calls queued
+    behind a GPU spin long enough that the GPU never waits for the host, so
+    the loop's wall time divided by `launches` is the host's own cost."""
+    import torch
+    from newt_amd import workloads as W
+    x, y = seeded(1_000_000, 0), seeded(1_000_000, 1)
+    o = torch.empty_like(x)
+    out = {}
+    for name, fn in (("newt", lambda: W.add(x, y, o)), ("torch", lambda: torch.add(x, y, out=o))):
+        for _ in range(50):
+            fn()
+        reps = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            torch.cuda._sleep(LEAD_CYCLES * 20)
+            t0 = time.perf_counter()
+            for _ in range(launches):
+                fn()
+            reps.append((time.perf_counter() - t0) / launches * 1e6)
+            torch.cuda.synchronize()
+        out[name] = round(min(reps), 2)
+    return {"workload": "host launch cost: add n=1e6 via @newt.jit (value) and torch.add(out=)",
+            "value": out["newt"], "unit": "us/launch", "torch_add_us": out["torch"],
+            "launches": launches}
+
+
 def secondary(cpu=True, cpu_budget=2.0):
     import torch
     from newt_amd import workloads as W
@@ -789,6 +819,7 @@ def secondary(cpu=True, cpu_budget=2.0):
                                                   rows=None if S <= 2048 else 512)
             res.append(line)
             del a, b, c
+        res.append(host_launch_cost())
         S = 4096
         # deuteron: the same matmul written as tiles, traced to newt and
         # autotuned against its eager oracle (examples/deuteron/01_matmul.py)

@@ -2,6 +2,8 @@
 
   * libnewt_hip.so - the C-ABI backend boundary (include/newt_hip.h): host C++
     over libamdhip64 + a run-time-loaded hipRTC. No device code, so g++ builds it.
+  * _newt_launch - the warm-launch path of @newt.jit in C (a CPython extension
+    that calls newt_launch_packed); gcc builds it.
   * device-template check - the gfx950 device header (csrc/device/newt_gfx950.h)
     is compiled offline with hipcc for gfx950, instantiating every template the
     code generator emits, so a broken header fails the build instead of the
@@ -35,6 +37,19 @@ def build_library():
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__",
           f"-I{ROCM}/include", f"-I{ROOT}/include", src, "-o", tmp, f"-L{ROCM}/lib",
           "-lamdhip64", "-ldl", "-Wl,--no-undefined"])
+    os.replace(tmp, out)
+    return out
+
+
+def build_launcher():
+    """The warm-launch path of @newt.jit (csrc/newt_pylaunch.c), a CPython
+    extension: it resolves newt_launch_packed in libnewt_hip.so at init."""
+    import sysconfig
+    src = os.path.join(CSRC, "newt_pylaunch.c")
+    out = os.path.join(CSRC, "_newt_launch" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out + ".tmp"
+    _run(["gcc", "-O2", "-fPIC", "-shared", "-Wall", "-Werror", "-std=c11",
+          f"-I{sysconfig.get_paths()['include']}", src, "-o", tmp, "-ldl"])
     os.replace(tmp, out)
     return out
 
@@ -94,6 +109,9 @@ def build(verbose=True):
     lib = build_library()
     if verbose:
         print("built", lib)
+    launcher = build_launcher()
+    if verbose:
+        print("built", launcher)
     co = check_device_header()
     if verbose:
         print("device header compiled for gfx950:", co)

@@ -191,6 +191,18 @@ _ARG_FMT = {"ptr": ("Q", 8), "i64": ("q", 8), "i32": ("i", 4), "f32": ("f", 4),
             "bool": ("?", 1), "f64": ("d", 8)}
 
 
+def pack_layout(kinds):
+    """(byte offset of each parameter, segment size) of the packed argument
+    segment pack_format lays out."""
+    offs, off = [], 0
+    for k in kinds:
+        size = struct.calcsize("=" + _ARG_FMT[k][0])
+        off += (-off) % _ARG_FMT[k][1]
+        offs.append(off)
+        off += size
+    return offs, off + (-off) % 8
+
+
 def pack_format(kinds):
     """struct format (explicit padding) laying out params with natural alignment."""
     fmt = "="

@@ -46,6 +46,60 @@ _CODEGEN_ENV = ("NEWT_VEC", "NEWT_PIPELINE_DOT", "NEWT_LDS_DMA", "NEWT_MFMA", "N
 _CODEGEN_ENV_B = tuple(k.encode() for k in _CODEGEN_ENV)
 
 
+class _Dev:
+    """The current device and stream, read the way a launch needs them: the
+    first call goes through torch.cuda (which initialises the runtime), later
+    ones through torch's raw accessors (no Stream object per launch)."""
+
+    ready = False
+
+    @classmethod
+    def device(cls):
+        import torch
+        if cls.ready:
+            return torch._C._cuda_getDevice()
+        d = torch.cuda.current_device()
+        cls.ready = True
+        return d
+
+    @staticmethod
+    def stream(device):
+        import torch
+        return torch._C._cuda_getCurrentRawStream(device)
+
+
+# the warm-launch path in C (csrc/newt_pylaunch.c): None until first use, then
+# the module, or False where it is not built (launches then stay in Python)
+_C_LAUNCH = None
+_C_KINDS = {"ptr": 0, "f32": 1, "i32": 2, "i64": 3, "bool": 4}
+
+
+def _c_launcher():
+    global _C_LAUNCH
+    if _C_LAUNCH is None:
+        _C_LAUNCH = False
+        if os.environ.get("NEWT_C_LAUNCH", "1") == "0":
+            return False
+        import importlib.machinery
+        import importlib.util
+        import sysconfig
+
+        import torch
+        path = os.path.join(os.path.dirname(_hip.LIB_PATH),
+                            "_newt_launch" + sysconfig.get_config_var("EXT_SUFFIX"))
+        if not os.path.exists(path):
+            return False
+        _hip.lib()   # the backend library first: the launcher resolves its entry point
+        loader = importlib.machinery.ExtensionFileLoader("_newt_launch", path)
+        spec = importlib.util.spec_from_file_location("_newt_launch", path, loader=loader)
+        mod = importlib.util.module_from_spec(spec)
+        loader.exec_module(mod)
+        mod.init(_hip.LIB_PATH, torch._C._cuda_getDevice, torch._C._cuda_getCurrentRawStream,
+                 os.environ._data, _CODEGEN_ENV_B, torch.Tensor)
+        _C_LAUNCH = mod
+    return _C_LAUNCH
+
+
 def _env_snapshot():
     """The codegen switches as a tuple, read without os.environ's per-key
     string encoding (a launch reads it on every call)."""
@@ -170,7 +224,8 @@ class CompiledKernel:
         self.kernel = _hip.Kernel(self.code, name, lds_bytes)
 
     def launch(self, grid, values, stream):
-        gx, gy, gz = (tuple(grid) + (1, 1, 1))[:3]
+        """grid: (gx, gy, gz) workgroups; values: the parameters in order."""
+        gx, gy, gz = grid
         ev = launch_events
         if ev is None:
             self.kernel.launch_packed(gx, gy, gz, 64 * self.num_warps, stream,
@@ -197,6 +252,8 @@ class JITFunction:
         self.cache = {}
         # launch fast path: call signature -> (CompiledKernel, argument plan)
         self._fast = {}
+        # the C launcher's plans: its call key -> plan
+        self._ctable = {}
         self._cx_pos = tuple(n in self.constexpr_names for n in self.param_names)
 
     def __getitem__(self, grid):
@@ -279,9 +336,11 @@ class JITFunction:
         constexprs, runtime = self._classify(args, kwargs)
         types = {n: self._type_of(n, v) for n, v in runtime.items()}
         key = self._key(constexprs, types, num_warps, num_stages, waves_per_eu)
+        # a code object is loaded into the current device: one entry per device
+        key = key + (_Dev.device(),)
         ck = self.cache.get(key)
         if ck is None:
-            ck = self._compile(key, constexprs, types, num_warps, num_stages, waves_per_eu)
+            ck = self._compile(key[:-1], constexprs, types, num_warps, num_stages, waves_per_eu)
             self.cache[key] = ck
         return ck
 
@@ -294,42 +353,138 @@ class JITFunction:
 
     def _call_signature(self, args, kwargs, opts):
         """A cheap, hashable summary of everything a launch specializes on:
-        per argument its kind, dtype, 16-byte alignment, device, int32 range,
-        ==1 and power-of-two divisibility (the value itself for constexprs),
-        plus the launch options and the codegen switches. Raises TypeError for
-        an unhashable constexpr value."""
+        the launch options and current device (opts), the codegen switches,
+        and per argument its dtype, 16-byte alignment and device (tensors),
+        ==1, power-of-two divisibility and int32 range (ints), or type and
+        value (constexprs). Raises TypeError for an unhashable constexpr."""
         import torch
 
+        Tensor = torch.Tensor
         cx = self._cx_pos
+        ncx = len(cx)
         out = [opts, _env_snapshot()]
+        append = out.append
         for i, v in enumerate(args):
-            out.append(("C", type(v), v) if i < len(cx) and cx[i] else _arg_sig(v, torch))
+            if i < ncx and cx[i]:
+                append((type(v), v))
+                continue
+            t = type(v)
+            if t is int:
+                append((v == 1, min(v & -v, 16) if v else 16, -2147483648 <= v < 2147483648))
+            elif t is float:
+                append(float)
+            elif t is Tensor or isinstance(v, Tensor):
+                # dtypes are singletons: their id stands for them (cheaper to
+                # hash); get_device() is the device index (-1 on the CPU)
+                append((id(v.dtype), not v.data_ptr() & 15, v.get_device()))
+            else:
+                append((t, v))
         for k, v in kwargs.items():
-            out.append((k, ("C", type(v), v) if k in self.constexpr_names else _arg_sig(v, torch)))
+            append((k, (type(v), v) if k in self.constexpr_names else _arg_sig(v, torch)))
         sig = tuple(out)
         hash(sig)
         return sig
 
-    def _plan(self, ck, args, kwargs):
-        """Where each kernel parameter's value comes from on a fast launch."""
-        pos = {n: i for i, n in enumerate(self.param_names[:len(args)])}
-        plan = []
-        for name, p in ck.params:
-            kind = 0 if isinstance(p.dtype, tp.pointer_type) else (1 if p.dtype == tp.float32 else 2)
-            if name in pos:
-                plan.append((0, pos[name], kind))
-            elif name in kwargs:
-                plan.append((1, name, kind))
-            else:
-                plan.append((2, self.defaults[name], kind))
-        return ck, tuple(plan)
-
-    def _run(self, grid, *args, **kwargs):
+    def _plan(self, ck, args, kwargs, device):
+        """The fast launch of this call signature: the compiled kernel and a
+        function from (args, kwargs) to the kernel's parameter values, in the
+        kernel's parameter order. Every tensor argument is checked here to be
+        on the current device: the signature records each tensor's device and
+        the current one, so a launch that reuses the plan needs no check."""
         import torch
 
+        bound = dict(zip(self.param_names, args))
+        bound.update(kwargs)
+        for name, v in bound.items():
+            if isinstance(v, torch.Tensor) and v.device.index not in (None, device):
+                raise ValueError(f"tensor '{name}' is on {v.device} but the current device is "
+                                 f"cuda:{device}; newt launches on the current device")
+        pos = {n: i for i, n in enumerate(self.param_names[:len(args)])}
+        items, consts = [], {}
+        for name, p in ck.params:
+            if name in pos:
+                src = f"a[{pos[name]}]"
+            elif name in kwargs:
+                src = f"k[{name!r}]"
+            else:
+                consts[f"_d{len(consts)}"] = self.defaults[name]
+                src = f"_d{len(consts) - 1}"
+            if isinstance(p.dtype, tp.pointer_type):
+                items.append(f"{src}.data_ptr()")
+            elif p.dtype == tp.float32:
+                items.append(f"float({src})")
+            else:
+                items.append(src)
+        # one generated expression instead of a loop over the parameters
+        values = eval(f"lambda a, k: ({', '.join(items)}{',' if len(items) == 1 else ''})",
+                      consts)
+        return ck, values
+
+    def _run(self, grid, *args, **kwargs):
+        ckey = None
+        C = _C_LAUNCH if _C_LAUNCH is not None else _c_launcher()
+        if C and _Dev.ready and launch_events is None:
+            try:
+                r = C.run(self._ctable, self._cx_pos, grid, args, kwargs)
+            except TypeError:     # an unhashable constexpr: the Python path reports it
+                r = False
+            if r is None:
+                return
+            if type(r) is int:
+                _hip._check(r, "hipModuleLaunchKernel")
+            if type(r) is tuple:
+                ckey = r
         num_warps = kwargs.pop("num_warps", 4)
         num_stages = kwargs.pop("num_stages", 3)
-        waves_per_eu = int(kwargs.pop("waves_per_eu", 0))
+        waves_per_eu = kwargs.pop("waves_per_eu", 0)
+        try:
+            device = _Dev.device()
+        except (RuntimeError, AssertionError):
+            device = None   # no GPU: the slow path reports argument errors first
+        try:
+            csig = self._call_signature(args, kwargs, (num_warps, num_stages, waves_per_eu,
+                                                       device))
+        except TypeError:
+            csig = None
+        fast = self._fast.get(csig) if csig is not None else None
+        if fast is None:
+            fast = self._slow_path(args, kwargs, num_warps, num_stages, waves_per_eu, device)
+            if csig is not None:
+                self._fast[csig] = fast
+        ck, values = fast
+        if callable(grid):
+            meta = dict(self.defaults)
+            meta.update(zip(self.param_names, args))
+            meta.update(kwargs)
+            meta["num_warps"] = num_warps
+            grid = grid(meta)
+        if type(grid) is not tuple:
+            grid = (grid,) if isinstance(grid, int) else tuple(grid)
+        if len(grid) == 1:
+            g = (int(grid[0]), 1, 1)
+        else:
+            g = (tuple(int(x) for x in grid) + (1, 1))[:3]
+        if g[0] <= 0 or g[1] <= 0 or g[2] <= 0:
+            return  # empty grid: no-op
+        ck.launch(g, values(args, kwargs), _Dev.stream(device))
+        if ckey is not None:
+            self._register_c_plan(ckey, ck, args)
+
+    def _register_c_plan(self, ckey, ck, args):
+        """Hand the C launcher a plan for this call signature when every
+        kernel parameter comes from a positional argument."""
+        pos = {n: i for i, n in enumerate(self.param_names[:len(args)])}
+        if not hasattr(ck, "kernel") or any(n not in pos for n, _ in ck.params):
+            return
+        offs, size = _hip.pack_layout(ck.kinds)
+        slots = tuple((pos[n], _C_KINDS[k], o) for (n, _), k, o in zip(ck.params, ck.kinds, offs))
+        self._ctable[ckey] = _C_LAUNCH.make_plan(ck.kernel.func.value or 0, 64 * ck.num_warps,
+                                                 size, slots)
+
+    def _slow_path(self, args, kwargs, num_warps, num_stages, waves_per_eu, device):
+        """First launch of a call signature: option checks, binding, types,
+        the specialization (compiled on a cache miss) and its launch plan."""
+        waves_per_eu = int(waves_per_eu)
         if not 0 <= waves_per_eu <= 8:
             raise ValueError(f"waves_per_eu must be in 0..8 (0 = no request), got {waves_per_eu}")
         if num_warps not in (1, 2, 4, 8, 16):
@@ -337,57 +492,21 @@ class JITFunction:
                              f"workgroup, at most 1024 threads), got {num_warps}")
         if not 1 <= num_stages <= 8:
             raise ValueError(f"num_stages must be in 1..8, got {num_stages}")
-        try:
-            csig = self._call_signature(args, kwargs, (num_warps, num_stages, waves_per_eu))
-        except TypeError:
-            csig = None
-        fast = self._fast.get(csig) if csig is not None else None
-        if fast is None:
-            constexprs, runtime = self._classify(args, kwargs)
-            types = {n: self._type_of(n, v) for n, v in runtime.items()}
-            key = self._key(constexprs, types, num_warps, num_stages, waves_per_eu)
-            ck = self.cache.get(key)
-            if ck is None:
-                ck = self._compile(key, constexprs, types, num_warps, num_stages, waves_per_eu)
-                self.cache[key] = ck
-            fast = self._plan(ck, args, kwargs)
-            if csig is not None:
-                self._fast[csig] = fast
-        ck, plan = fast
-        values = []
-        dev = None
-        for src, ref, kind in plan:
-            v = args[ref] if src == 0 else (kwargs[ref] if src == 1 else ref)
-            if kind == 0:
-                if dev is None:
-                    dev = torch.cuda.current_device()
-                if v.device.index not in (None, dev):
-                    raise ValueError(
-                        f"tensor is on {v.device} but the current device is "
-                        f"cuda:{dev}; newt launches on the current device")
-                values.append(v.data_ptr())
-            elif kind == 1:
-                values.append(float(v))
-            else:
-                values.append(v)
-        if callable(grid):
-            meta = dict(self.defaults)
-            meta.update(zip(self.param_names, args))
-            meta.update(kwargs)
-            meta["num_warps"] = num_warps
-            g = grid(meta)
-        else:
-            g = grid
-        if isinstance(g, int):
-            g = (g,)
-        g = tuple(int(x) for x in g)
-        if any(x <= 0 for x in g):
-            return  # empty grid: no-op
-        stream = torch.cuda.current_stream().cuda_stream
-        ck.launch(g, values, stream)
+        constexprs, runtime = self._classify(args, kwargs)
+        types = {n: self._type_of(n, v) for n, v in runtime.items()}
+        if device is None:
+            import torch
+            device = torch.cuda.current_device()   # raises the runtime's own error
+        key = self._key(constexprs, types, num_warps, num_stages, waves_per_eu) + (device,)
+        ck = self.cache.get(key)
+        if ck is None:
+            ck = self._compile(key[:-1], constexprs, types, num_warps, num_stages, waves_per_eu)
+            self.cache[key] = ck
+        return self._plan(ck, args, kwargs, device)
 
 
 def _arg_sig(v, torch):
+    """_call_signature's entry for a runtime argument passed by keyword."""
     t = type(v)
     if t is int:
         return ("i", v == 1, _pow2_div(v), -(2 ** 31) <= v < 2 ** 31)
@@ -396,7 +515,7 @@ def _arg_sig(v, torch):
     if t is bool:
         return "b"
     if isinstance(v, torch.Tensor):
-        return (v.dtype, v.data_ptr() % 16 == 0, v.device)
+        return (id(v.dtype), v.data_ptr() % 16 == 0, v.get_device())
     return ("?", t, v)
 
 

@@ -89,3 +89,27 @@ def test_device_is_gfx950():
     assert device_arch(0).startswith("gfx950")
     cus, lds, ws = device_limits(0)
     assert ws == 64 and cus >= 256 and lds >= 64 * 1024
+
+
+@pytest.mark.gpu
+def test_warm_launches_take_the_c_path():
+    """The first launch of a call signature runs in Python and registers a
+    plan with the C launcher; later launches with the same signature (other
+    tensors and values, same facts) run through it, with the same results."""
+    from newt_amd import workloads as W
+    from newt_amd.runtime import jit as J
+    g = torch.Generator().manual_seed(3)
+    x, y = (torch.randn(4096, generator=g).cuda() for _ in range(2))
+    W.add(x, y)
+    if not J._C_LAUNCH:
+        pytest.skip("the C launcher is not built")
+    n = len(W.add_kernel._ctable)
+    assert n >= 1
+    for size in (4096, 4004, 8192):
+        a, b = (torch.randn(size, generator=g).cuda() for _ in range(2))
+        out = W.add(a, b)
+        torch.cuda.synchronize()
+        assert torch.equal(out, a + b), size
+    # 4004 differs from 4096 in its divisibility (4, not 16), 8192 does not:
+    # one new plan
+    assert len(W.add_kernel._ctable) == n + 1
