@@ -63,8 +63,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--config", default=None, help="BM,BN,BK,warps,stages (skip autotune)")
     ap.add_argument("--only", default=None,
-                    help="run one workload for profiler runs: 'matmul', 'copy', or the "
-                         "start of a secondary workload's name (e.g. 'softmax fp32 4096x4096')")
+                    help="run one workload for profiler runs: 'matmul', 'copy' (torch's "
+                         "device copy, counter calibration), 'newt copy' (the copy ceiling's "
+                         "kernel at 128 MiB moved), or the start of a secondary workload's "
+                         "name (e.g. 'softmax fp32 4096x4096')")
     ap.add_argument("--operands", default="random", choices=("random", "constant", "bf16-values"),
                     help="with --only matmul: the configuration's N(0,1)/sqrt(K) operands "
                          "(random), every element 1/64 (constant), or the random values "
@@ -576,6 +578,17 @@ def run_only(name):
             dst.copy_(src)
         torch.cuda.synchronize()
         log("copy: 5 x 256 MiB device-to-device copies")
+        return
+    if name.startswith("newt copy"):
+        # the copy ceiling's kernel at 128 MiB moved (the layernorm's bytes)
+        from newt_amd import workloads as W
+        src = torch.ones(128 << 20 >> 3, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            W.copy(src, dst)
+        torch.cuda.synchronize()
+        assert torch.equal(dst, src)
+        log("newt copy: 10 x 128 MiB moved (64 MiB read, 64 MiB written)")
         return
     for wl in _secondary_workloads():
         if wl["name"].startswith(name):
