@@ -206,7 +206,12 @@ def c_launch(tmp_path):
         stream, func = ctypes.c_void_p(), ctypes.c_void_p()
         n = stub.stub_last(buf, rec, ctypes.byref(stream), ctypes.byref(func))
         return bytes(buf[:n]), tuple(rec[:5]), stream.value, func.value
-    return mod, stub, last
+    yield mod, stub, last
+    # the extension's state is per process: if this process set up the real
+    # launcher, bind it back to libnewt_hip.so and torch
+    if J._C_LAUNCH:
+        J._C_LAUNCH = None
+        J._c_launcher()
 
 
 def test_c_launch_packs_what_the_python_path_packs(c_launch):
