@@ -474,12 +474,12 @@ class JITFunction:
         """Hand the C launcher a plan for this call signature when every
         kernel parameter comes from a positional argument."""
         pos = {n: i for i, n in enumerate(self.param_names[:len(args)])}
-        if not hasattr(ck, "kernel") or any(n not in pos for n, _ in ck.params):
+        func = getattr(getattr(ck, "kernel", None), "func", None)
+        if not (func and func.value) or any(n not in pos for n, _ in ck.params):
             return
         offs, size = _hip.pack_layout(ck.kinds)
         slots = tuple((pos[n], _C_KINDS[k], o) for (n, _), k, o in zip(ck.params, ck.kinds, offs))
-        self._ctable[ckey] = _C_LAUNCH.make_plan(ck.kernel.func.value or 0, 64 * ck.num_warps,
-                                                 size, slots)
+        self._ctable[ckey] = _C_LAUNCH.make_plan(func.value, 64 * ck.num_warps, size, slots)
 
     def _slow_path(self, args, kwargs, num_warps, num_stages, waves_per_eu, device):
         """First launch of a call signature: option checks, binding, types,
