@@ -469,10 +469,12 @@ def summarize(head, lines):
     """Every measured configuration in one small object: per workload the
     value, its unit, the fraction of the peak that bounds it (HBM 8 TB/s or
     the dense MFMA peak; for memory-bound lines do_bench-timed), the
-    kernel-only fraction on flushed caches (dispatch events) where measured,
-    and the torch CPU eager baseline's value in the same unit."""
+    kernel-only fraction on flushed caches (dispatch events; the headline's
+    flushed median) where measured, and the torch CPU eager baseline's value
+    in the same unit."""
     rows = {"matmul fp16 4096^3 (headline)": [
-        head["value"], "TFLOP/s", head["roofline"]["frac"], None,
+        head["value"], "TFLOP/s", head["roofline"]["frac"],
+        round(head["tflops_flushed_median"] / PEAK_TFLOPS, 4),
         head.get("cpu_baseline", {}).get("value")]}
     for line in lines:
         if "workload" not in line:

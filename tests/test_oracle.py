@@ -337,7 +337,7 @@ def test_layernorm_violations_accept_fp32_and_reject_mistakes():
     w = (1 + 0.1 * rng.standard_normal(N)).astype(np.float16).astype(np.float32)
     b = (0.1 * rng.standard_normal(N)).astype(np.float16).astype(np.float32)
     y, mean, rstd = _fp32_layernorm(x, w, b, 1e-5)
-    for dt in ("float16", "float32"):
+    for dt in ("float16", "bfloat16", "float32"):
         got = orc.round_to(y, dt)
         assert orc.layernorm_violations(got, mean, rstd, x, w, b, 1e-5, dt) == \
             {"y": 0, "mean": 0, "rstd": 0}
@@ -358,6 +358,10 @@ def test_layernorm_violations_accept_fp32_and_reject_mistakes():
     flip = y16.copy()
     flip[3, 5] = -flip[3, 5] if abs(flip[3, 5]) > 1e-3 else 1.0
     assert orc.layernorm_violations(flip, mean, rstd, x, w, b, 1e-5, "float16")["y"] == 1
+    # bf16: two ulps off fails
+    yb = orc.round_to(y, "bfloat16")
+    assert orc.layernorm_violations(yb + np.abs(yb) * 2.0 ** -6, mean, rstd, x, w, b, 1e-5,
+                                    "bfloat16")["y"] > y.size // 2
     # fp32 output: the same planted offsets fail the term-scaled rtol
     assert orc.layernorm_violations(y * (1 + 1e-4), mean, rstd, x, w, b, 1e-5,
                                     "float32")["y"] > y.size // 2
