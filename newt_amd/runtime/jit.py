@@ -423,6 +423,11 @@ class JITFunction:
     def _run(self, grid, *args, **kwargs):
         ckey = None
         C = _C_LAUNCH if _C_LAUNCH is not None else _c_launcher()
+        if C and not _Dev.ready:
+            try:
+                _Dev.device()       # initialises the runtime once, through torch
+            except (RuntimeError, AssertionError):
+                pass                # no GPU: the Python path reports what is wrong
         if C and _Dev.ready and launch_events is None:
             try:
                 r = C.run(self._ctable, self._cx_pos, grid, args, kwargs)

@@ -113,3 +113,41 @@ def test_warm_launches_take_the_c_path():
     # 4004 differs from 4096 in its divisibility (4, not 16), 8192 does not:
     # one new plan
     assert len(W.add_kernel._ctable) == n + 1
+
+
+import newt_amd as newt  # noqa: E402
+import newt_amd.language as nl  # noqa: E402
+
+
+@newt.jit
+def kinds_k(x_ptr, o_ptr, a, n, big, flag, BLOCK: nl.constexpr):
+    offs = nl.program_id(0) * BLOCK + nl.arange(0, BLOCK)
+    m = offs < n
+    x = nl.load(x_ptr + offs, mask=m)
+    shift = (big >> 36).to(nl.float32)        # an int64 beyond int32's range
+    y = a * x + shift
+    if flag:
+        y = -y
+    nl.store(o_ptr + offs, y, mask=m)
+
+
+@pytest.mark.gpu
+def test_c_path_packs_every_argument_kind():
+    """A kernel with pointer, fp32, int32, int64 and bool parameters: the
+    first launch runs in Python, the second and third through the C launcher
+    (same call signature, other values); every launch computes what torch
+    computes from the same values."""
+    from newt_amd.runtime import jit as J
+
+    g = torch.Generator().manual_seed(5)
+    for i, (a, big, flag) in enumerate(((1.5, 3 << 36, True), (-2.0, 5 << 36, False),
+                                        (0.25, 7 << 36, True))):
+        x = torch.randn(1000, generator=g).cuda()
+        o = torch.empty_like(x)
+        kinds_k[(4,)](x, o, a, 1000, big, flag, BLOCK=256)
+        torch.cuda.synchronize()
+        want = a * x + float(big >> 36)
+        want = -want if flag else want
+        assert torch.equal(o, want), i
+    if J._C_LAUNCH:
+        assert len(kinds_k._ctable) == 1
