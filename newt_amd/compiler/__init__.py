@@ -109,7 +109,7 @@ def _streamed(fndef, kinds):
     """ids of the top-level calls named in `kinds` (nl.load / nl.store) that
     touch data no other program touches: the address depends on every
     program axis the kernel uses (one row per program, as in softmax or
-    layernorm), the call is not inside a loop (no re-reads) and a load's value
+    layernorm), the call is inside no loop, at any depth (no re-reads), and a load's value
     does not feed nl.dot (dot operands are shared by the programs of a row or
     column of tiles). Their lines need not stay in the caches, so they take
     the non-temporal hint; data shared by all programs (a layernorm's weight
@@ -124,12 +124,14 @@ def _streamed(fndef, kinds):
         return set()
     dot_names = {a.id for n in ast.walk(fndef) if _callee_name(n) == "dot"
                  for a in ast.walk(n) if isinstance(a, ast.Name)}
+    in_loops = {id(n) for st in ast.walk(fndef) if isinstance(st, (ast.For, ast.While))
+                for n in ast.walk(st)}
     out = set()
     for st in fndef.body:
         if isinstance(st, (ast.For, ast.While)):
             continue
         for n in ast.walk(st):
-            if _callee_name(n) not in kinds or not n.args:
+            if _callee_name(n) not in kinds or not n.args or id(n) in in_loops:
                 continue
             if isinstance(st, ast.Assign) and any(isinstance(t, ast.Name) and t.id in dot_names
                                                   for t in st.targets):

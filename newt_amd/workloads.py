@@ -16,9 +16,12 @@ reference's examples/01-05), extended to the benchmark configurations:
                     to the diagonal, p cast to V's dtype before P @ V, and the
                     softmax written on exp2 with log2(e) folded into the scale
                     (exp(x) = exp2(x*log2 e): the same softmax, fewer
-                    instructions per element); launched with waves_per_eu=2 so
-                    two waves share each SIMD and one wave's softmax runs while
-                    the other's MFMAs do
+                    instructions per element), the exponents referred to each
+                    row's first-block maximum (no rescale in the main loops;
+                    an online-softmax pass for a program where some row's sum
+                    passes 2^80 or the accumulator overflows); launched with
+                    waves_per_eu=2 so two waves share each SIMD and one
+                    wave's softmax runs while the other's MFMAs do
   attention_plain_kernel
                     examples/05_fused_attention.py:14-48 as written there
                     (nl.exp, qk * scale, a where mask), generalised only by the
@@ -246,38 +249,37 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
     q = nl.load(q_base + offs_m[:, None] * sqm + offs_d[None, :], mask=qmask, other=0.0)
 
     qk_scale = scale * 1.4426950408889634  # log2(e): the softmax runs on exp2
-    m_i = nl.full((BLOCK_M,), float("-inf"), dtype=nl.float32)
+    # The exponents share one reference point per row, m_i: the row's maximum
+    # over the first key block, fixed for the rest of the row. O = acc / l_i
+    # is the same quotient whatever reference point the exponents share, so
+    # the loops never rescale acc: p = exp2(qk * s - m_i) only grows past 1
+    # where a later score exceeds the first block's maximum. While every p
+    # stays below 2^80, l_i stays far inside fp32's range; a row whose sum l_i
+    # passes 2^80 (some score 80 or more above that maximum, in log2 units),
+    # or an acc that overflowed, sends the program through the online-softmax
+    # loop at the end, which rescales at every block. (A rescale inside the
+    # main loops costs a cross-wave maximum, a barrier and a branch per key
+    # block.)
+    m_i = nl.zeros((BLOCK_M,), dtype=nl.float32)
     l_i = nl.zeros((BLOCK_M,), dtype=nl.float32)
     acc = nl.zeros((BLOCK_M, D), dtype=nl.float32)
 
     # key blocks wholly inside the sequence (and, causal, wholly below the
     # diagonal of every row of this program) need no mask; the ragged tail and
     # the diagonal blocks run in a second, masked loop. Scores stay unscaled:
-    # the scale is applied inside the exponent's fma, and the running max is
+    # the scale is applied inside the exponent's fma, and the reference is
     # max(qk) * qk_scale (= max(qk * qk_scale): rounding is monotonic).
     full_n = S // BLOCK_N * BLOCK_N
     end_n = S
     if CAUSAL:
         full_n = nl.minimum(full_n, pid * BLOCK_M // BLOCK_N * BLOCK_N)
         end_n = nl.minimum(S, (pid + 1) * BLOCK_M)
-    #
-    # The running maximum m_i moves only when some row's block maximum passes
-    # it by more than 8 (in log2 units): until then p = exp2(qk * s - m_i)
-    # stays <= 2^8, and acc and l_i keep their scale, so the per-block
-    # rescale of acc (64 multiplies per lane) runs only on the blocks that
-    # move it (the first, and rarely another). O = acc / l_i is the same
-    # quotient whichever reference point the exponents share.
     for start_n in range(0, full_n, BLOCK_N):
         offs_n = start_n + nl.arange(0, BLOCK_N)
         k = nl.load(k_base + offs_n[:, None] * skn + offs_d[None, :])
         qk = nl.dot(q, nl.trans(k))
-        m_blk = nl.max(qk, axis=1) * qk_scale
-        if nl.max(m_blk - m_i) > 8.0:
-            m_new = nl.maximum(m_i, m_blk)
-            alpha = nl.exp2(m_i - m_new)
-            l_i = l_i * alpha
-            acc = acc * alpha[:, None]
-            m_i = m_new
+        if start_n == 0:
+            m_i = nl.max(qk, axis=1) * qk_scale
         p = nl.exp2(nl.fma(qk, qk_scale, -m_i[:, None]))
         l_i = l_i + nl.sum(p, axis=1)
         v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :])
@@ -292,20 +294,44 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
                           qk, float("-inf"))
         else:
             qk = nl.where(offs_n[None, :] < S, qk, float("-inf"))
-        # a row whose keys are all masked here has m_blk = -inf: it never
-        # moves the maximum, and its p is exp2(-inf) = 0 (every row has a
-        # finite m_i from the first key block on: key 0 is never masked)
-        m_blk = nl.max(qk, axis=1) * qk_scale
-        if nl.max(m_blk - m_i) > 8.0:
-            m_new = nl.maximum(m_i, m_blk)
-            alpha = nl.exp2(m_i - m_new)
-            l_i = l_i * alpha
-            acc = acc * alpha[:, None]
-            m_i = m_new
+        # the first key block has key 0 in it, which no row masks: every row's
+        # reference is finite (masked scores are -inf, p = exp2(-inf) = 0)
+        if start_n == 0:
+            m_i = nl.max(qk, axis=1) * qk_scale
         p = nl.exp2(nl.fma(qk, qk_scale, -m_i[:, None]))
         l_i = l_i + nl.sum(p, axis=1)
         v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :], mask=nmask, other=0.0)
         acc = nl.dot(p.to(v_ptr.dtype.element_ty), v, acc)
+
+    # acc <= l_i * max|v|: past the first block's maximum, p grows acc by up
+    # to 2^80 more than the per-block rescale's p <= 1 does, so for values
+    # above ~2^48 acc can overflow where the rescaled sum stays finite.
+    # acc * 0 is NaN exactly where acc holds an inf or NaN (no fast-math:
+    # the product is not folded), which makes `peak` NaN and sends the
+    # program through the rescaling pass too.
+    peak = nl.max(l_i) + nl.sum(acc * 0.0)
+    if not (peak <= 1.2089258196146292e24):  # 2^80: start again with a rescale per block
+        m_i = nl.full((BLOCK_M,), float("-inf"), dtype=nl.float32)
+        l_i = nl.zeros((BLOCK_M,), dtype=nl.float32)
+        acc = nl.zeros((BLOCK_M, D), dtype=nl.float32)
+        for start_n in range(0, end_n, BLOCK_N):
+            offs_n = start_n + nl.arange(0, BLOCK_N)
+            nmask = offs_n[:, None] < S
+            k = nl.load(k_base + offs_n[:, None] * skn + offs_d[None, :], mask=nmask, other=0.0)
+            qk = nl.dot(q, nl.trans(k))
+            if CAUSAL:
+                qk = nl.where((offs_m[:, None] >= offs_n[None, :]) & (offs_n[None, :] < S),
+                              qk, float("-inf"))
+            else:
+                qk = nl.where(offs_n[None, :] < S, qk, float("-inf"))
+            m_new = nl.maximum(m_i, nl.max(qk, axis=1) * qk_scale)
+            alpha = nl.exp2(m_i - m_new)
+            p = nl.exp2(nl.fma(qk, qk_scale, -m_new[:, None]))
+            l_i = l_i * alpha + nl.sum(p, axis=1)
+            acc = acc * alpha[:, None]
+            v = nl.load(v_base + offs_n[:, None] * svn + offs_d[None, :], mask=nmask, other=0.0)
+            acc = nl.dot(p.to(v_ptr.dtype.element_ty), v, acc)
+            m_i = m_new
 
     acc = acc / l_i[:, None]
     nl.store(o_base + offs_m[:, None] * som + offs_d[None, :], acc.to(o_ptr.dtype.element_ty),
@@ -372,13 +398,13 @@ def attention(q, k, v, causal=False, scale=None, out=None, BLOCK_M=None, BLOCK_N
     exponent and takes max(qk) * scale as the row maximum, which holds only
     for a positive scale.
 
-    Default tiles: 32 query rows per wave, two waves per SIMD. Non-causal
-    programs take 256 rows on 8 waves (one workgroup per CU then shares each K
-    and V block between all 8 waves: ~1.3% faster than two workgroups of 128
-    rows at [4,32,4096,128]); causal ones 128 rows on 4 waves (256-row blocks
-    waste more work on the diagonal and balance worse: 7% slower)."""
+    Default tiles: 32 query rows per wave, two waves per SIMD, 256-row
+    programs on 8 waves (one workgroup per CU shares each K and V block
+    between all 8 waves); causal too, where two 128-row workgroups per CU
+    measured 2-3% slower (their register budget spills around the
+    online-softmax pass)."""
     if BLOCK_M is None:
-        BLOCK_M = 128 if causal else 256
+        BLOCK_M = 256
     if num_warps is None:
         num_warps = BLOCK_M // 32
     B, H, S, D = q.shape

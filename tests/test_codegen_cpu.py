@@ -435,10 +435,12 @@ def test_loops_reusing_a_target_name_compile():
 
 
 def test_sequential_pipelined_loops_share_lds_stages():
-    """Attention's unmasked key loop and its masked tail loop are both
-    pipelined (direct-to-LDS copies, branch-free fast copy), and the second
-    reuses the first one's stage arrays after a barrier: the kernel needs the
-    LDS of one loop (2 stages x (K + V) = 64 KiB), not of two."""
+    """Attention's unmasked key loop, its masked tail loop and the
+    online-softmax pass it takes for rows whose scores outgrow the first
+    block's maximum are all pipelined (direct-to-LDS copies, branch-free fast
+    copy), and each reuses the previous one's stage arrays after a barrier:
+    the kernel needs the LDS of one loop (2 stages x (K + V) = 64 KiB), not
+    of three."""
     args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
     args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})
     for n in ("sqb", "sqh", "sqm", "skb", "skh", "skn", "svb", "svh", "svn", "sob", "soh", "som"):
@@ -447,10 +449,10 @@ def test_sequential_pipelined_loops_share_lds_stages():
         src, lds = compile_source(W.attention_kernel, args,
                                   {"BLOCK_M": 128, "BLOCK_N": 64, "D": 128, "CAUSAL": causal},
                                   num_warps=4, num_stages=2, waves_per_eu=2)
-        # + the cross-wave partials of the maximum test (two buffers per loop):
-        # two programs still fit one CU's 160 KiB
+        # + the cross-wave partials of the reductions: two programs still fit
+        # one CU's 160 KiB
         assert 64 * 1024 <= lds <= 64 * 1024 + 1024
-        assert len(re.findall(r"for \(; _it\d+ \+ 2 <", src)) == 2   # two fast copies
+        assert len(re.findall(r"for \(; _it\d+ \+ 2 <", src)) == 3   # three fast copies
         assert src.count("newt::lds_dma16(") >= 16
 
 

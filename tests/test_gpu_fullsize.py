@@ -24,9 +24,9 @@ samples it so that every program of the launch is touched:
              fp32 unit of mean(|x|) for rows whose sum cancels, rstd rtol
              1e-5 (oracle.layernorm_violations).
   attention  (the default kernel and the examples/05 plain form) every
-             (batch, head) pair, one query row of every 128-row block (the
-             causal launch's programs; the non-causal ones own two such
-             blocks) at an offset that cycles through the block and moves
+             (batch, head) pair, one query row of every 128-row block (each
+             256-row program of the default launch owns two such blocks, a
+             128-row one exactly one) at an offset that cycles through the block and moves
              with the pair, plus every row of the first, a middle and the
              last block of eight pairs spread over all 128: relative
              Frobenius error <= 1e-2 per row and per pair
@@ -79,7 +79,7 @@ def test_matmul_square_autotuned(W, S, dtype):
     assert bad == 0, f"{bad} of {got.size} sampled elements beyond one ulp"
 
 
-QUERY_BLOCK = 128   # the smaller of the two query-block sizes launched (128 causal, 256 not)
+QUERY_BLOCK = 128   # at most the query rows of one program (the default launches 256)
 
 
 @pytest.mark.parametrize("plain", [False, True], ids=["default", "plain_form"])

@@ -13,6 +13,7 @@ oracle/newt_oracle.py at the tolerance north_star states:
   matmul, attention (fp16/bf16): relative Frobenius error <= 1e-2
 """
 
+import math
 import numpy as np
 import pytest
 import torch
@@ -244,13 +245,64 @@ def test_attention(W, causal, B, H, S, D):
 @pytest.mark.parametrize("B,H,S,D", [(1, 2, 256, 128), (2, 2, 300, 128), (1, 1, 1000, 128),
                                      (1, 2, 64, 128)])
 def test_attention_default_config(W, causal, B, H, S, D):
-    """The configuration bench.py and users get (BLOCK_M=128, BLOCK_N=64, 4
+    """The configuration bench.py and users get (BLOCK_M=256, BLOCK_N=64, 8
     waves, 2 stages, waves_per_eu=2), including ragged sequence lengths."""
     q, k, v = (seeded((B, H, S, D), s, dtype=torch.bfloat16) for s in (16, 17, 18))
     o = W.attention(q, k, v, causal=causal)
     ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
                         out_dtype="bfloat16")
     assert orc.rel_frobenius(npf(o), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("growth,S", [(20.0, 1000), (4.0, 777), (200.0, 513)])
+def test_attention_scores_outgrowing_the_first_block(W, causal, growth, S):
+    """The default kernel refers every exponent to a row's first-block
+    maximum; keys whose norms grow along the sequence (by 1 + j / growth)
+    push later scores far past it, so rows' sums pass 2^80 and the programs
+    take the online-softmax pass (a growth of 200 stays below it: both
+    paths are checked). Every row matches the oracle."""
+    B, H, D = 1, 2, 128
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(B, H, S, D, generator=g)
+    k = torch.randn(B, H, S, D, generator=g) * (1 + torch.arange(S) / growth)[None, None, :, None]
+    v = torch.randn(B, H, S, D, generator=g)
+    q, k, v = (t.bfloat16().cuda() for t in (q, k, v))
+    o = W.attention(q, k, v, causal=causal)
+    assert torch.isfinite(o).all()
+    ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    got = npf(o)
+    worst = max(orc.rel_frobenius(got[0, h, r], ref[0, h, r]) for h in range(H) for r in range(S))
+    assert worst <= 1e-2, worst
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_large_values_with_rising_scores(W, causal):
+    """Scores that rise linearly along the keys, to 2^40 (head 0) and 2^70
+    (head 1) above the first key block's maximum in log2 units, over values
+    in [2^110, 2^111): every row's sum l stays below 2^80, but with the
+    exponents referred to the first block's maximum p * v passes fp32's
+    range, where a per-block rescale keeps p <= 1 and the sums finite (at
+    most S * 2^111). The kernel finds the overflow in its accumulator and
+    takes the online-softmax pass; every row matches the oracle."""
+    B, H, S, D = 1, 2, 1000, 128
+    rise = torch.tensor([40.0, 70.0], dtype=torch.float64)       # log2 units over the keys
+    slope = rise * math.log(2.0) / S                              # natural-log units per key
+    score = slope[:, None] * torch.arange(S, dtype=torch.float64)[None, :]   # [H, S]
+    # q = 1 everywhere; k_j = (score_j / sqrt(D)) everywhere gives q.k * D^-0.5 = score_j
+    q = torch.ones(B, H, S, D)
+    k = (score / math.sqrt(D))[None, :, :, None].expand(B, H, S, D).float()
+    g = torch.Generator().manual_seed(12)
+    v = (1.0 + torch.rand(B, H, S, D, generator=g)) * 2.0 ** 110
+    q, k, v = (t.bfloat16().cuda() for t in (q, k, v))
+    o = W.attention(q, k, v, causal=causal)
+    assert torch.isfinite(o).all()
+    ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    got = npf(o)
+    worst = max(orc.rel_frobenius(got[0, h, r], ref[0, h, r]) for h in range(H) for r in range(S))
+    assert worst <= 1e-2, worst
 
 
 def test_attention_golden(W):
