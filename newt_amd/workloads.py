@@ -232,11 +232,27 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
                      BLOCK_M: nl.constexpr, BLOCK_N: nl.constexpr, D: nl.constexpr,
                      CAUSAL: nl.constexpr):
     pid = nl.program_id(0)
-    if CAUSAL:
-        # query block i does i + 1 key blocks: launch the heaviest first so the
-        # last programs to start are short ones (a shorter tail)
-        pid = nl.num_programs(0) - 1 - pid
     bh = nl.program_id(1)
+    if CAUSAL:
+        # Query block i does i + 1 key blocks: each XCD should start its
+        # heaviest programs first, so that the last to start are short ones
+        # (longest-processing-time-first order, a short tail). Program ids
+        # arrive renumbered so that each XCD runs one contiguous range of
+        # lin = pid + nqb * bh in increasing order; when the heads split evenly
+        # over the 8 XCDs that range is gh whole heads, which it would run one
+        # after another, heaviest to lightest within each. Renumbering the
+        # range's r-th program to weight rank r // gh of head r % gh runs every
+        # head's heaviest block, then every head's next, and so on. (Any
+        # bijection of the programs computes the same result.)
+        nqb = nl.num_programs(0)
+        nbh = nl.num_programs(1)
+        if nbh % 8 == 0:
+            gh = nbh // 8
+            lin = pid + nqb * bh
+            r = lin % (gh * nqb)
+            bh = lin // (gh * nqb) * gh + r % gh
+            pid = r // gh
+        pid = nqb - 1 - pid
     bi = bh // H
     hi = bh % H
     q_base = q_ptr + bi * sqb + hi * sqh

@@ -254,6 +254,25 @@ def test_attention_default_config(W, causal, B, H, S, D):
     assert orc.rel_frobenius(npf(o), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("B,H,S", [(1, 8, 1000), (2, 8, 300), (3, 8, 777), (1, 24, 513)])
+def test_attention_causal_heads_split_over_xcds(W, B, H, S):
+    """Causal launches whose B*H heads split evenly over the 8 XCDs take the
+    heaviest-first renumbering of programs (every head's last query block
+    first); each (batch, head, query block) must still be computed exactly
+    once: the output starts as NaN and every row is held to the oracle."""
+    D = 128
+    q, k, v = (seeded((B, H, S, D), s, dtype=torch.bfloat16) for s in (40, 41, 42))
+    o = torch.full_like(q, float("nan"))
+    W.attention(q, k, v, causal=True, out=o)
+    got = npf(o)
+    assert np.isfinite(got).all()
+    ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, True, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    worst = max(orc.rel_frobenius(got[b, h, r], ref[b, h, r])
+                for b in range(B) for h in range(H) for r in range(S))
+    assert worst <= 1e-2, worst
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("growth,S", [(20.0, 1000), (4.0, 777), (200.0, 513)])
 def test_attention_scores_outgrowing_the_first_block(W, causal, growth, S):
