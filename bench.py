@@ -78,7 +78,19 @@ def parse():
                     help="with --only matmul: per-workgroup start, end-of-k-loop and end "
                          "timestamps of the headline kernel (s_memrealtime, 100 MHz), "
                          "summarised per XCD")
+    ap.add_argument("--torch-mm", action="store_true",
+                    help="with --only matmul --power: run torch.mm (hipBLASLt) on the same "
+                         "operands instead of the newt kernel, for the power comparison")
+    ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
+                    help="with --only: afterwards run the workload back to back for SECONDS "
+                         "of GPU time while a thread reads the GPU's socket power, energy "
+                         "counter, graphics clocks and power-limit accounting through "
+                         "amdsmi; prints one JSON line of the summary")
     args = ap.parse_args()
+    if args.power and not args.only:
+        ap.error("--power applies to --only runs")
+    if args.torch_mm and not (args.power and args.only == "matmul"):
+        ap.error("--torch-mm applies to --only matmul --power runs")
     if args.timeline and args.only != "matmul":
         ap.error("--timeline applies to --only matmul runs")
     if args.dtype != "fp16" and args.only != "matmul":
@@ -235,6 +247,114 @@ def settle_clocks(fn, seconds):
     return {"launches": done, "gpu_s": round(spent, 3)}
 
 
+class PowerSampler:
+    """The GPU's power state while kernels run, read through amdsmi (ROCm's
+    SMI library: it reads the power-management firmware's metrics table from
+    the driver and makes no HIP call). A thread reads the metrics table (socket
+    power, per-XCD graphics clocks) every `period` seconds; the violation
+    accounting (the firmware's count of the ~1 ms intervals in which the
+    package power limit, PPT, or a temperature limit held the clock below the
+    host's limit) is read at the start and end of the window. The firmware's
+    energy counter is not read: over windows of a few seconds its averages
+    disagreed with the power samples and exceeded the cap."""
+
+    _sm = None
+
+    def __init__(self, period=0.005):
+        import threading
+        if PowerSampler._sm is None:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            PowerSampler._sm = amdsmi
+        self.sm = PowerSampler._sm
+        self.h = self._handle()
+        self.period = period
+        self.samples = []
+        self.stop = threading.Event()
+        self.thread = threading.Thread(target=self._run, daemon=True)
+
+    def _handle(self):
+        import torch
+        hs = self.sm.amdsmi_get_processor_handles()
+        if len(hs) == 1:
+            return hs[0]
+        bus = getattr(torch.cuda.get_device_properties(0), "pci_bus_id", None)
+        for h in hs:
+            if bus is not None and int(self.sm.amdsmi_get_gpu_device_bdf(h).split(":")[1], 16) == bus:
+                return h
+        raise RuntimeError(f"PowerSampler: {len(hs)} GPUs visible to amdsmi and none matches "
+                           f"cuda:0's PCI bus {bus}")
+
+    def _state(self):
+        v = self.sm.amdsmi_get_violation_status(self.h)
+        st = {"t": time.perf_counter()}
+        for k in ("acc_counter", "acc_ppt_pwr", "acc_socket_thrm", "acc_vr_thrm",
+                  "acc_hbm_thrm"):
+            st[k] = v[k]
+        return st
+
+    def _run(self):
+        while not self.stop.is_set():
+            m = self.sm.amdsmi_get_gpu_metrics_info(self.h)
+            self.samples.append((time.perf_counter(), m["current_socket_power"],
+                                 m["current_gfxclks"]))
+            self.stop.wait(self.period)
+
+    def __enter__(self):
+        self.first = self._state()
+        self.thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self.stop.set()
+        self.thread.join()
+        self.last = self._state()
+
+    def summary(self, skip_s=0.5):
+        """Power and clocks over the window after its first `skip_s` seconds
+        (the steady state); the violation accounting over the whole window."""
+        a, b = self.first, self.last
+        steady = [s for s in self.samples if s[0] >= a["t"] + skip_s] or self.samples
+        watts = sorted(s[1] for s in steady if isinstance(s[1], (int, float)))
+        clocks = sorted(c for s in steady if isinstance(s[2], list)
+                        for c in s[2] if isinstance(c, (int, float)) and c > 0)
+        n = b["acc_counter"] - a["acc_counter"]
+        frac = lambda k: (round((b[k] - a[k]) / n, 4)
+                          if n and b.get(k) is not None and a.get(k) is not None else None)
+        pct = lambda xs, q: xs[min(len(xs) - 1, int(len(xs) * q))] if xs else None
+        return {
+            "window_s": round(b["t"] - a["t"], 3), "steady_samples": len(steady),
+            "socket_power_w_p10_p50_p90": [pct(watts, 0.1), pct(watts, 0.5), pct(watts, 0.9)],
+            "power_cap_w": self.sm.amdsmi_get_power_cap_info(self.h)["power_cap"] / 1e6,
+            "gfxclk_mhz_p10_p50_p90": [pct(clocks, 0.1), pct(clocks, 0.5), pct(clocks, 0.9)],
+            "violation_intervals": n,
+            "ppt_limited_frac": frac("acc_ppt_pwr"),
+            "thermal_limited_frac": frac("acc_socket_thrm"),
+            "vr_thermal_limited_frac": frac("acc_vr_thrm"),
+            "hbm_thermal_limited_frac": frac("acc_hbm_thrm"),
+        }
+
+
+def power_window(name, fn, seconds, flop=None, nbytes=None):
+    """Run fn back to back for `seconds` of GPU time under a PowerSampler,
+    with an idle window of the same sampler before it; print one JSON line."""
+    import torch
+    torch.cuda.synchronize()
+    time.sleep(0.5)
+    with PowerSampler() as idle:
+        time.sleep(1.0)
+    with PowerSampler() as ps:
+        ran = settle_clocks(fn, seconds)
+    out = {"power": name, "launches": ran["launches"], "gpu_s": ran["gpu_s"],
+           "idle": idle.summary(), "busy": ps.summary()}
+    per = ran["gpu_s"] / ran["launches"]
+    if flop:
+        out["tflops"] = round(flop / per / 1e12, 1)
+    if nbytes:
+        out["gbs"] = round(nbytes / per / 1e9, 1)
+    print(json.dumps(out), flush=True)
+
+
 def cpu_info():
     """This host's CPU model and physical core count (from /proc/cpuinfo),
     logical CPUs, the CPUs this process may run on and torch's threads."""
@@ -355,7 +475,7 @@ def main():
     import torch
     torch.cuda.set_device(0)
     if args.only and args.only != "matmul":
-        return run_only(args.only)
+        return run_only(args.only, args.power)
     from newt_amd import workloads as W
     from newt_amd.testing import _flush_buffer
 
@@ -415,6 +535,13 @@ def main():
         log(f"matmul only ({args.dtype} {S}^3, {cfg}, {args.operands} operands): "
             f"{value:.1f} TFLOP/s, "
             f"{statistics.median(kern_list) * 1e3:.2f} us per launch with dispatch events")
+        if args.power:
+            if args.torch_mm:
+                step = lambda: torch.mm(a, b, out=c)
+                name = f"torch.mm (hipBLASLt) {args.dtype} {S}^3 {args.operands} operands"
+            else:
+                name = f"matmul {args.dtype} {S}^3 {args.operands} operands {cfg}"
+            power_window(name, step, args.power, flop=flop)
         return
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
@@ -570,8 +697,9 @@ def matmul_timeline(a, b, c, cfg, step, launches=40, keep=30):
             f"(min {min(lp):.2f}, max {max(lp):.2f}), C store median {statistics.median(stv):.2f} us")
 
 
-def run_only(name):
-    """One workload for profiler runs (counters / kernel traces)."""
+def run_only(name, power=0.0):
+    """One workload for profiler runs (counters / kernel traces); with
+    `power`, then that many seconds of it under the PowerSampler."""
     import torch
     if name == "copy":
         src = torch.ones(64 << 20, device="cuda")
@@ -599,6 +727,10 @@ def run_only(name):
             torch.cuda.synchronize()
             wl["check"]()
             log(f"{name}: ran {wl['name']}")
+            if power:
+                flops = wl["name"].startswith("attention")
+                power_window(wl["name"], wl["fn"], power, flop=wl["work"] if flops else None,
+                             nbytes=None if flops else wl["work"])
             return
     raise SystemExit(f"bench.py: no workload named {name!r}")
 
