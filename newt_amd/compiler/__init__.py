@@ -169,6 +169,165 @@ def _shares_across_programs(fndef):
     return False
 
 
+def _work_grows_along_axis0(fndef, constexprs):
+    """True when a program's work grows with its program_id(0): the trip
+    count of some outermost for-loop is a non-decreasing function of axis 0
+    that depends on it (a causal attention's key loop, bounded by its query
+    block's diagonal), no outermost loop's count is anything else but
+    independent of axis 0, and the kernel has no atomics (so the order in
+    which programs run cannot be observed). Such a grid is best run heaviest
+    first: every program that starts late is then a short one.
+
+    An abstract interpretation over the statements in order gives each name
+    'C' (independent of axis 0), 'I' (non-decreasing in it and dependent on
+    it), 'D' (non-increasing) or 'U' (unknown). Constexpr ifs take their live
+    branch, a runtime if joins its branches, and names assigned inside a loop
+    are 'U' after it."""
+
+    def const_value(e):
+        # compile-time value of an expression over literals and constexprs
+        if isinstance(e, ast.Constant) and isinstance(e.value, (int, float, bool)):
+            return e.value
+        if isinstance(e, ast.Name) and e.id in constexprs:
+            v = constexprs[e.id]
+            return getattr(v, "value", v)
+        if isinstance(e, ast.UnaryOp):
+            v = const_value(e.operand)
+            if v is None:
+                return None
+            return {ast.USub: lambda: -v, ast.Not: lambda: not v, ast.UAdd: lambda: v}.get(
+                type(e.op), lambda: None)()
+        if isinstance(e, ast.BinOp):
+            a, b = const_value(e.left), const_value(e.right)
+            if a is None or b is None:
+                return None
+            ops = {ast.Add: lambda: a + b, ast.Sub: lambda: a - b, ast.Mult: lambda: a * b,
+                   ast.FloorDiv: lambda: a // b if b else None, ast.Mod: lambda: a % b if b else None}
+            return ops.get(type(e.op), lambda: None)()
+        if isinstance(e, ast.BoolOp):
+            vs = [const_value(x) for x in e.values]
+            if any(v is None for v in vs):
+                return None
+            return all(vs) if isinstance(e.op, ast.And) else any(vs)
+        if isinstance(e, ast.Compare) and len(e.ops) == 1:
+            a, b = const_value(e.left), const_value(e.comparators[0])
+            if a is None or b is None:
+                return None
+            ops = {ast.Eq: a == b, ast.NotEq: a != b, ast.Lt: a < b, ast.LtE: a <= b,
+                   ast.Gt: a > b, ast.GtE: a >= b}
+            return ops.get(type(e.ops[0]))
+        return None
+
+    def positive(e):
+        v = const_value(e)
+        return isinstance(v, (int, float)) and not isinstance(v, bool) and v > 0
+
+    def add(a, b):
+        if a == "C":
+            return b
+        if b == "C":
+            return a
+        return a if a == b and a in ("I", "D") else "U"
+
+    neg = {"C": "C", "I": "D", "D": "I", "U": "U"}
+    atomics = [False]
+
+    def ev(e, env):
+        name = _callee_name(e) if isinstance(e, ast.Call) else None
+        if name == "program_id":
+            arg = e.args[0] if e.args else next((k.value for k in e.keywords if k.arg == "axis"), None)
+            ax = const_value(arg) if arg is not None else None
+            return "I" if ax == 0 else ("C" if ax in (1, 2) else "U")
+        if name in ("minimum", "maximum", "min", "max") and len(e.args) == 2 and not e.keywords:
+            a, b = ev(e.args[0], env), ev(e.args[1], env)
+            return add(a, b) if "U" not in (a, b) else "U"
+        if name == "cdiv" and len(e.args) == 2 and positive(e.args[1]):
+            return ev(e.args[0], env)
+        if isinstance(e, ast.Name):
+            return env.get(e.id, "C")
+        if isinstance(e, ast.Constant):
+            return "C"
+        if isinstance(e, ast.UnaryOp) and isinstance(e.op, ast.USub):
+            return neg[ev(e.operand, env)]
+        if isinstance(e, ast.BinOp):
+            a, b = ev(e.left, env), ev(e.right, env)
+            if isinstance(e.op, ast.Add):
+                return add(a, b)
+            if isinstance(e.op, ast.Sub):
+                return add(a, neg[b])
+            if isinstance(e.op, ast.Mult):
+                if a == "C" and b == "C":
+                    return "C"
+                if a == "C" and positive(e.left):
+                    return b
+                if b == "C" and positive(e.right):
+                    return a
+                return "U"
+            if isinstance(e.op, ast.FloorDiv) and b == "C" and positive(e.right):
+                return a
+            return "C" if a == b == "C" else "U"
+        # anything else is independent of axis 0 only if all of its parts are
+        parts = [x for x in ast.iter_child_nodes(e) if isinstance(x, ast.expr)]
+        return "C" if all(ev(x, env) == "C" for x in parts) else "U"
+
+    def assigned(stmts):
+        out = set()
+        for st in stmts:
+            for n in ast.walk(st):
+                if isinstance(n, (ast.Assign, ast.AugAssign, ast.AnnAssign, ast.For)):
+                    tgts = n.targets if isinstance(n, ast.Assign) else [n.target]
+                    for t in tgts:
+                        out |= {x.id for x in ast.walk(t) if isinstance(x, ast.Name)}
+        return out
+
+    counts = []
+
+    def walk(stmts, env):
+        for st in stmts:
+            for n in ast.walk(st):
+                if _callee_name(n) in ("atomic_add", "atomic_max", "atomic_min"):
+                    atomics[0] = True
+            if isinstance(st, ast.Assign):
+                v = ev(st.value, env)
+                for t in st.targets:
+                    names = [x.id for x in ast.walk(t) if isinstance(x, ast.Name)]
+                    for nm in names:
+                        env[nm] = v if isinstance(t, ast.Name) else "U"
+            elif isinstance(st, ast.AugAssign) and isinstance(st.target, ast.Name):
+                env[st.target.id] = ev(ast.BinOp(left=ast.Name(id=st.target.id, ctx=ast.Load()),
+                                                 op=st.op, right=st.value), env)
+            elif isinstance(st, ast.AnnAssign) and isinstance(st.target, ast.Name) and st.value:
+                env[st.target.id] = ev(st.value, env)
+            elif isinstance(st, ast.If):
+                c = const_value(st.test)
+                if c is not None:
+                    walk(st.body if c else st.orelse, env)
+                else:
+                    e1, e2 = dict(env), dict(env)
+                    walk(st.body, e1)
+                    walk(st.orelse, e2)
+                    for k in set(e1) | set(e2):
+                        a, b = e1.get(k, "C"), e2.get(k, "C")
+                        env[k] = a if a == b else "U"
+            elif isinstance(st, (ast.For, ast.While)):
+                cnt = "U"
+                if (isinstance(st, ast.For) and _callee_name(st.iter) == "range"
+                        and 1 <= len(st.iter.args) <= 3 and not st.iter.keywords):
+                    a = st.iter.args
+                    lo, hi = (ast.Constant(0), a[0]) if len(a) == 1 else (a[0], a[1])
+                    if len(a) < 3 or positive(a[2]):
+                        cnt = add(ev(hi, env), neg[ev(lo, env)])
+                counts.append(cnt)
+                for nm in assigned([st]):
+                    env[nm] = "U"
+            else:
+                for nm in assigned([st]):
+                    env[nm] = "U"
+
+    walk(fndef.body, {})
+    return not atomics[0] and "I" in counts and all(c in ("C", "I") for c in counts)
+
+
 _MEM_WRITES = {"store", "atomic_add", "atomic_max", "atomic_min"}
 
 
@@ -253,6 +412,7 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
     prefer_rows = _has_row_reduction(fndef)
     group_pids = _split_dot_axes(fndef)
     remap_pids = _shares_across_programs(fndef)
+    lpt_pids = _work_grows_along_axis0(fndef, constexprs)
     # NEWT_NT_LOAD=1 / NEWT_NT_STREAM=1 read / write program-private streams
     # with the non-temporal hint. Measured on streaming kernels of 32-256 MB:
     # loads +2-4% under XCD-renumbered program order but 1-4% slower in the
@@ -275,6 +435,7 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
         cg.group_pids = group_pids
         cg.stream_loads = stream_loads
         cg.remap_pids = remap_pids
+        cg.lpt_pids = lpt_pids
         cg.stream_stores = stream_stores
         try:
             src = cg.compile()

@@ -203,6 +203,7 @@ class Codegen(ast.NodeVisitor):
         self.pid_remap = False
         self.group_pids = False   # set by compile_fn for matmul-shaped kernels
         self.remap_pids = True    # compile_fn: False when no data is shared by a subset of programs
+        self.lpt_pids = False     # compile_fn: True when a program's work grows with program_id(0)
         self.params = params
         vec = 1
         for _, p in params:
@@ -1718,7 +1719,17 @@ class Codegen(ast.NodeVisitor):
         inside a group: the 32 or so programs an XCD runs at once then share
         G row panels and about 32/G column panels instead of needing every
         row panel, which keeps an 8192^3 fp16 matmul's operands in L2/MALL
-        (NEWT_PID_GROUP=G, default 4; 0 turns grouping off)."""
+        (NEWT_PID_GROUP=G, default 4; 0 turns grouping off).
+
+        In a kernel whose work grows with program_id(0) (lpt_pids: a causal
+        attention's key loop ends at its query block's diagonal), the
+        programs run heaviest first, the longest-processing-time-first order
+        that keeps short programs for the end of the launch. When the grid's
+        other axes split evenly over the 8 XCDs, each XCD's range holds gh
+        whole rows of axis 0 (gh heads); its r-th program becomes weight rank
+        r / gh of row r % gh, counted from the heaviest, so every row's
+        heaviest program starts first, then every row's next. Otherwise axis
+        0 is reversed within each row (NEWT_PID_LPT=0 turns this off)."""
         ax = self._cx(node, axis, "program_id axis")
         if os.environ.get("NEWT_PID_REMAP", "1") == "0" or not self.remap_pids:
             return self.new_scalar(tp.int32, f"(int)blockIdx.{'xyz'[ax]}")
@@ -1732,6 +1743,18 @@ class Codegen(ast.NodeVisitor):
                 "  if (_pb < _full) _pb = (_pb & 7u) * (_full >> 3) + (_pb >> 3); }",
             ]
             G = int(os.environ.get("NEWT_PID_GROUP", "4")) if self.group_pids else 0
+            if G == 0 and self.lpt_pids and os.environ.get("NEWT_PID_LPT", "1") != "0":
+                self.prologue += [
+                    "{ const unsigned _nh = _nb / _nbx;",
+                    "  if (_nh % 8u == 0u) {",
+                    "    const unsigned _gh = _nh >> 3, _per = _gh * _nbx, _base = _pb / _per * _per, "
+                    "_r = _pb - _base;",
+                    "    _pb = _base + (_r % _gh) * _nbx + (_nbx - 1u - _r / _gh);",
+                    "  } else {",
+                    "    const unsigned _p0 = _pb % _nbx;",
+                    "    _pb = _pb - _p0 + (_nbx - 1u - _p0);",
+                    "  } }",
+                ]
             if G > 0:
                 self.prologue += [
                     f"const unsigned _q = _pb % (_nbx * _nby), _gw = {G}u * _nby;",

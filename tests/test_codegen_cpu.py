@@ -398,6 +398,123 @@ def test_program_id_mapping_is_a_bijection(monkeypatch, tmp_path, group):
         assert r.returncode == 0, (g, r.returncode)
 
 
+_PID_ORDER_HARNESS = r"""
+#include <stdio.h>
+#include <stdlib.h>
+struct dim { unsigned x, y, z; };
+int main(int argc, char **argv) {
+  const struct dim gridDim = {atoi(argv[1]), atoi(argv[2]), atoi(argv[3])};
+  const unsigned n = gridDim.x * gridDim.y * gridDim.z;
+  for (unsigned b = 0; b < n; b++) {
+    const struct dim blockIdx = {b %% gridDim.x, b / gridDim.x %% gridDim.y, b / (gridDim.x * gridDim.y)};
+%s
+    printf("%%u %%d %%d %%d\n", b, _pid0, _pid1, _pid2);
+  }
+  return 0;
+}
+"""
+
+
+def _plain_attention_prologue(causal):
+    src, _ = compile_source(W.attention_plain_kernel, _attention_args(),
+                            {"BLOCK_M": 256, "BLOCK_N": 64, "D": 128, "CAUSAL": causal},
+                            num_warps=8, num_stages=2, waves_per_eu=2)
+    lines = src.splitlines()
+    i0 = next(i for i, l in enumerate(lines) if "const unsigned _nbx" in l)
+    i1 = next(i for i, l in enumerate(lines) if "const int _pid2" in l)
+    return "\n".join(lines[i0:i1 + 1])
+
+
+def test_work_growing_along_axis0_detected():
+    """The causal examples/05 form's key loop ends at its query block's
+    diagonal, so its work grows with program_id(0); the hand-written kernel
+    numbers its programs itself, and loops independent of axis 0, shrinking
+    with it, of unknown sign, or in kernels with atomics are not matched."""
+    from newt_amd.compiler import _work_grows_along_axis0 as grows
+    f = lambda k: fndef_of(k)[0]
+    assert grows(f(W.attention_plain_kernel), {"CAUSAL": True, "BLOCK_M": 256, "BLOCK_N": 64})
+    assert not grows(f(W.attention_plain_kernel), {"CAUSAL": False, "BLOCK_M": 256, "BLOCK_N": 64})
+    for causal in (True, False):
+        assert not grows(f(W.attention_kernel), {"CAUSAL": causal, "BLOCK_M": 256, "BLOCK_N": 64})
+    for k, cex in ((W.matmul_kernel, {"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 32}),
+                   (W.softmax_kernel, {"BLOCK_N": 1024}), (W.layernorm_kernel, {"BLOCK_N": 1024}),
+                   (W.add_kernel, {"BLOCK": 1024})):
+        assert not grows(f(k), cex)
+
+    def tri(o_ptr, n, stride, B: nl.constexpr):
+        pid = nl.program_id(0)
+        acc = 0.0
+        for i in range(0, (pid + 1) * B):
+            acc += 1.0
+        nl.store(o_ptr + pid, acc)
+
+    def shrinking(o_ptr, n, B: nl.constexpr):
+        pid = nl.program_id(0)
+        for i in range(pid * B, n):
+            pass
+
+    def unknown_sign(o_ptr, n, stride, B: nl.constexpr):
+        pid = nl.program_id(0)
+        for i in range(0, pid * stride):
+            pass
+
+    def with_atomics(o_ptr, n, B: nl.constexpr):
+        pid = nl.program_id(0)
+        for i in range(0, nl.minimum(n, pid + 1)):
+            nl.atomic_add(o_ptr, 1.0)
+
+    def runtime_join(o_ptr, n, B: nl.constexpr):
+        pid = nl.program_id(0)
+        end = n
+        if n > 4:
+            end = pid
+        for i in range(0, end):
+            pass
+
+    def other_axis(o_ptr, n, B: nl.constexpr):
+        for i in range(0, nl.program_id(1) * B):
+            pass
+
+    assert grows(f(tri), {"B": 4})
+    assert not grows(f(tri), {"B": 0})
+    for k in (shrinking, unknown_sign, with_atomics, runtime_join, other_axis):
+        assert not grows(f(k), {"B": 4}), k.__name__
+
+
+def test_heaviest_first_program_ids(tmp_path):
+    """The causal examples/05 form is compiled with the heaviest-first
+    prologue (the non-causal form without it). Built with gcc and run over
+    every workgroup id: a bijection on even and ragged grids; on a grid whose
+    heads split evenly over the 8 XCDs, the workgroups each XCD receives
+    (linear ids b = x, x + 8, ...) take every head's heaviest query block
+    (pid0 = nbx - 1) first, then every head's next, over the XCD's whole heads."""
+    pro = _plain_attention_prologue(True)
+    assert "_nbx - 1u - _r / _gh" in pro
+    assert "_nbx - 1u" not in _plain_attention_prologue(False)
+    c = tmp_path / "pid.c"
+    c.write_text(_PID_HARNESS % pro)
+    exe = tmp_path / "pid"
+    subprocess.run(["gcc", "-O1", "-o", str(exe), str(c)], check=True)
+    for g in ((16, 128, 1), (16, 16, 1), (13, 7, 2), (5, 4, 1), (1, 1, 1), (3, 100, 1),
+              (100, 3, 1), (9, 9, 3), (1, 17, 1), (17, 1, 1), (16, 24, 1), (7, 8, 2)):
+        r = subprocess.run([str(exe)] + [str(v) for v in g])
+        assert r.returncode == 0, (g, r.returncode)
+    c2 = tmp_path / "order.c"
+    c2.write_text(_PID_ORDER_HARNESS % pro)
+    exe2 = tmp_path / "order"
+    subprocess.run(["gcc", "-O1", "-o", str(exe2), str(c2)], check=True)
+    for nbx, nby in ((16, 128), (8, 16), (5, 24)):
+        out = subprocess.run([str(exe2), str(nbx), str(nby), "1"], capture_output=True,
+                             text=True, check=True).stdout.split("\n")
+        rows = [tuple(map(int, l.split())) for l in out if l]
+        gh = nby // 8
+        for x in range(8):
+            seq = [(p0, p1) for b, p0, p1, _ in rows if b % 8 == x]
+            assert [p0 for p0, _ in seq] == [nbx - 1 - i // gh for i in range(len(seq))]
+            heads = {p1 for _, p1 in seq}
+            assert len(heads) == gh and heads == set(range(min(heads), min(heads) + gh))
+
+
 def test_attention_program_ids_not_grouped():
     args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
     args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})
