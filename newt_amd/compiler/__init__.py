@@ -173,10 +173,10 @@ def _work_grows_along_axis0(fndef, constexprs):
     """True when a program's work grows with its program_id(0): the trip
     count of some outermost for-loop is a non-decreasing function of axis 0
     that depends on it (a causal attention's key loop, bounded by its query
-    block's diagonal), no outermost loop's count is anything else but
-    independent of axis 0, and the kernel has no atomics (so the order in
-    which programs run cannot be observed). Such a grid is best run heaviest
-    first: every program that starts late is then a short one.
+    block's diagonal), every other outermost loop's count is independent of
+    axis 0, and the kernel has no atomics (so the order in which programs run
+    cannot be observed). Such a grid is best run heaviest first: every
+    program that starts late is then a short one.
 
     An abstract interpretation over the statements in order gives each name
     'C' (independent of axis 0), 'I' (non-decreasing in it and dependent on
