@@ -185,6 +185,9 @@ MATMUL_CONFIGS = [
     newt.Config({"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=8, num_stages=4),
     newt.Config({"BLOCK_M": 128, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=8, num_stages=4),
     newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=3),
+    # 2048^3 (one 128x128 tile per CU): 64-deep k-steps with 4 stages (128 KB)
+    # measured 813 against 799 TFLOP/s for the 32-deep tile below
+    newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=4),
     newt.Config({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=4, num_stages=4),
     newt.Config({"BLOCK_M": 64, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4, num_stages=3),
     # 64x64 tiles give a 1024^3 problem 256 workgroups (one per CU)
