@@ -243,18 +243,24 @@ def attention_kernel(q_ptr, k_ptr, v_ptr, o_ptr, S, H, scale,
         # arrive renumbered so that each XCD runs one contiguous range of
         # lin = pid + nqb * bh in increasing order; when the heads split evenly
         # over the 8 XCDs that range is gh whole heads, which it would run one
-        # after another, heaviest to lightest within each. Renumbering the
-        # range's r-th program to weight rank r // gh of head r % gh runs every
-        # head's heaviest block, then every head's next, and so on. (Any
+        # after another, heaviest to lightest within each. The range is taken
+        # in groups of grp = 4 heads (all gh when 4 does not divide gh), and
+        # within a group its r-th program becomes weight rank r // grp of head
+        # r % grp: every head's heaviest block, then every head's next, and so
+        # on, with four heads' keys and values in the XCD's L2 at a time. (Any
         # bijection of the programs computes the same result.)
         nqb = nl.num_programs(0)
         nbh = nl.num_programs(1)
         if nbh % 8 == 0:
             gh = nbh // 8
+            grp = gh
+            if gh % 4 == 0:
+                grp = 4
             lin = pid + nqb * bh
             r = lin % (gh * nqb)
-            bh = lin // (gh * nqb) * gh + r % gh
-            pid = r // gh
+            rr = r % (grp * nqb)
+            bh = lin // (gh * nqb) * gh + r // (grp * nqb) * grp + rr % grp
+            pid = rr // grp
         pid = nqb - 1 - pid
     bi = bh // H
     hi = bh % H

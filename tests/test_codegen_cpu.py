@@ -486,10 +486,11 @@ def test_heaviest_first_program_ids(tmp_path):
     prologue (the non-causal form without it). Built with gcc and run over
     every workgroup id: a bijection on even and ragged grids; on a grid whose
     heads split evenly over the 8 XCDs, the workgroups each XCD receives
-    (linear ids b = x, x + 8, ...) take every head's heaviest query block
-    (pid0 = nbx - 1) first, then every head's next, over the XCD's whole heads."""
+    (linear ids b = x, x + 8, ...) take its whole heads in groups of 4 (all
+    of them when 4 does not divide their count), and within a group every
+    head's heaviest query block (pid0 = nbx - 1) first, then every head's next."""
     pro = _plain_attention_prologue(True)
-    assert "_nbx - 1u - _r / _gh" in pro
+    assert "_nbx - 1u - _rr / _G" in pro
     assert "_nbx - 1u" not in _plain_attention_prologue(False)
     c = tmp_path / "pid.c"
     c.write_text(_PID_HARNESS % pro)
@@ -503,16 +504,20 @@ def test_heaviest_first_program_ids(tmp_path):
     c2.write_text(_PID_ORDER_HARNESS % pro)
     exe2 = tmp_path / "order"
     subprocess.run(["gcc", "-O1", "-o", str(exe2), str(c2)], check=True)
-    for nbx, nby in ((16, 128), (8, 16), (5, 24)):
+    for nbx, nby in ((16, 128), (8, 16), (5, 24), (4, 64)):
         out = subprocess.run([str(exe2), str(nbx), str(nby), "1"], capture_output=True,
                              text=True, check=True).stdout.split("\n")
         rows = [tuple(map(int, l.split())) for l in out if l]
         gh = nby // 8
+        G = 4 if gh % 4 == 0 else gh
         for x in range(8):
             seq = [(p0, p1) for b, p0, p1, _ in rows if b % 8 == x]
-            assert [p0 for p0, _ in seq] == [nbx - 1 - i // gh for i in range(len(seq))]
-            heads = {p1 for _, p1 in seq}
-            assert len(heads) == gh and heads == set(range(min(heads), min(heads) + gh))
+            assert len(seq) == gh * nbx
+            h0 = min(p1 for _, p1 in seq)
+            assert {p1 for _, p1 in seq} == set(range(h0, h0 + gh))
+            for i, (p0, p1) in enumerate(seq):
+                g, rr = divmod(i, G * nbx)
+                assert (p0, p1) == (nbx - 1 - rr // G, h0 + g * G + rr % G), (nbx, nby, x, i)
 
 
 def test_attention_program_ids_not_grouped():
