@@ -254,12 +254,15 @@ def test_attention_default_config(W, causal, B, H, S, D):
     assert orc.rel_frobenius(npf(o), ref) <= 1e-2
 
 
-@pytest.mark.parametrize("B,H,S", [(1, 8, 1000), (2, 8, 300), (3, 8, 777), (1, 24, 513)])
+@pytest.mark.parametrize("B,H,S", [(1, 8, 1000), (2, 8, 300), (3, 8, 777), (1, 24, 513),
+                                   (1, 32, 300), (2, 32, 300), (1, 96, 200)])
 def test_attention_causal_heads_split_over_xcds(W, B, H, S):
     """Causal launches whose B*H heads split evenly over the 8 XCDs take the
     heaviest-first renumbering of programs (every head's last query block
-    first); each (batch, head, query block) must still be computed exactly
-    once: the output starts as NaN and every row is held to the oracle."""
+    first, over groups of 4 of an XCD's heads when 4 divides their count: one,
+    two and three groups in the last three cases); each (batch, head, query
+    block) must still be computed exactly once: the output starts as NaN and
+    every row is held to the oracle."""
     D = 128
     q, k, v = (seeded((B, H, S, D), s, dtype=torch.bfloat16) for s in (40, 41, 42))
     o = torch.full_like(q, float("nan"))
