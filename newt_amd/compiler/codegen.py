@@ -694,6 +694,11 @@ class Codegen(ast.NodeVisitor):
             exprs = [self.scalar_expr(o) for o in operands]
             return self.new_scalar(rdtype, fn(exprs))
         ops = [self.expand_to_rank(o, len(shape)) if isinstance(o, Block) else o for o in operands]
+        # a load an earlier statement already brought into registers takes
+        # part as those registers, so its layout can be the result's; left as
+        # a load, a broadcast operand (a row statistic) would choose the
+        # layout and the whole loaded block would go through LDS to meet it
+        ops = [o.result if isinstance(o, LazyLoad) and o.result is not None else o for o in ops]
         regs = [o for o in ops if isinstance(o, (Reg, LazyLoad))]
         if not regs:
             size = 1 + sum(self.lazy_size(o) for o in ops)

@@ -520,6 +520,24 @@ def test_heaviest_first_program_ids(tmp_path):
                 assert (p0, p1) == (nbx - 1 - rr // G, h0 + g * G + rr % G), (nbx, nby, x, i)
 
 
+def test_loaded_block_keeps_its_layout_against_a_broadcast_statistic():
+    """A [1, N] row block that an earlier reduction already loaded, combined
+    with the broadcast row statistic (the traced softmax's
+    `row - row.amax(1)[:, None]`), keeps the load's 16-byte layout: the
+    block is not converted through LDS, and the store is vectorised."""
+    def k(x_ptr, o_ptr, N, BLOCK: nl.constexpr):
+        rows = nl.program_id(0) + nl.arange(0, 1)
+        cols = nl.arange(0, BLOCK)
+        x = nl.load(x_ptr + rows[:, None] * N + cols[None, :])
+        m = nl.max(x, axis=1)
+        nl.store(o_ptr + rows[:, None] * N + cols[None, :], x - m[:, None])
+
+    src, _ = compile_source(k, {"x_ptr": (F32P, A16), "o_ptr": (F32P, A16), "N": (tp.int32, D16)},
+                            {"BLOCK": 4096})
+    assert "_cv" not in src
+    assert "store_vec<float, 4>" in src
+
+
 def test_attention_program_ids_not_grouped():
     args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
     args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})
