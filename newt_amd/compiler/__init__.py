@@ -45,6 +45,33 @@ def _has_row_reduction(fndef):
     return False
 
 
+def _chained_dots(fndef):
+    """True when some nl.dot's first operand is computed from another dot's
+    result (attention's P @ V after S = Q K^T). Names are followed through
+    assignments anywhere in the function, to a fixed point, so loop-carried
+    dependences count."""
+    import ast
+    assigns = [n for n in ast.walk(fndef) if isinstance(n, (ast.Assign, ast.AugAssign))]
+
+    def reads(e):
+        return {x.id for x in ast.walk(e) if isinstance(x, ast.Name) and isinstance(x.ctx, ast.Load)}
+
+    fed = set()
+    changed = True
+    while changed:
+        changed = False
+        for a in assigns:
+            tgts = a.targets if isinstance(a, ast.Assign) else [a.target]
+            names = {t.id for t in tgts if isinstance(t, ast.Name)}
+            if names <= fed:
+                continue
+            if any(_callee_name(x) == "dot" for x in ast.walk(a.value)) or reads(a.value) & fed:
+                fed |= names
+                changed = True
+    return any(_callee_name(n) == "dot" and n.args and reads(n.args[0]) & fed
+               for n in ast.walk(fndef))
+
+
 def _split_dot_axes(fndef):
     """True when some nl.dot's first operand depends on program axis 0 but not
     axis 1 and its second on axis 1 but not axis 0 (or the reverse): the tiled
@@ -410,6 +437,7 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
     fed to the next until no new hint appears."""
     hints = {}
     prefer_rows = _has_row_reduction(fndef)
+    chained_dots = _chained_dots(fndef)
     group_pids = _split_dot_axes(fndef)
     remap_pids = _shares_across_programs(fndef)
     lpt_pids = _work_grows_along_axis0(fndef, constexprs)
@@ -432,6 +460,7 @@ def compile_fn(fndef, fn_globals, params, constexprs, num_warps, kernel_name, nu
         cg = Compiler(fndef, fn_globals, params, constexprs, num_warps, kernel_name,
                       num_stages=num_stages, hints=hints, waves_per_eu=waves_per_eu)
         cg.prefer_rows = prefer_rows
+        cg.chained_dots = chained_dots
         cg.group_pids = group_pids
         cg.stream_loads = stream_loads
         cg.remap_pids = remap_pids

@@ -52,6 +52,7 @@ def _choose_instr(M, N, K, dt, small_first=False):
 
 class DotOps:
     prefer_rows = False
+    chained_dots = False
 
     def wave_grid(self, M, N, instr):
         MI = lo.INSTR[instr][0]
@@ -92,16 +93,25 @@ class DotOps:
         return M, N, K, dt, instr, wm, wn, rep
 
     def pick_instr(self, M, N, K, dt):
-        """32x32x16, except for a column-oriented dot whose waves each hold a
-        tile of at least 128x128 over a single 32-deep k-step: there the
-        16x16x32 MFMA (same rate, half the latency) measured ~3.5% faster for
-        the 4-wave 256x256x32 matmul, while it is slower with more waves per
-        SIMD (their latency is already hidden) or with deeper k-steps
-        (register pressure). Row-oriented kernels keep 32x32x16 for their
-        in-register P @ V path."""
+        """32x32x16, except
+        - for a column-oriented dot whose waves each hold a tile of at least
+          128x128 over a single 32-deep k-step: there the 16x16x32 MFMA (same
+          rate, half the latency) measured ~3.5% faster for the 4-wave
+          256x256x32 matmul, while it is slower with more waves per SIMD
+          (their latency is already hidden) or with deeper k-steps (register
+          pressure);
+        - for every dot of a row-oriented kernel that feeds one dot's result
+          into another (flash attention): 16x16x32, whose accumulator feeds
+          the next MFMA from registers as 32x32x16's does. At the package
+          power limit it ran at an ~11% higher clock for the same power and
+          1-3.5% faster on seven of eight attention shapes (2% slower at 1024
+          causal keys). Other row-oriented kernels keep 32x32x16.
+        NEWT_MFMA=16 / 32 forces the shape wherever it fits."""
         instr = _choose_instr(M, N, K, dt)
+        mode = os.environ.get("NEWT_MFMA", "")
         if self.prefer_rows or instr != "32x32x16" or K != 32:
-            return _choose_instr(M, N, K, dt, small_first=os.environ.get("NEWT_MFMA") == "16")
+            small = mode == "16" or (self.prefer_rows and self.chained_dots and mode != "32")
+            return _choose_instr(M, N, K, dt, small_first=small)
         wm, wn, _ = self.wave_grid(M, N, instr)
         big = M // wm >= 128 and N // wn >= 128
         return _choose_instr(M, N, K, dt, small_first=big)

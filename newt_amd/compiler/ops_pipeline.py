@@ -227,15 +227,26 @@ class DotPipeline:
                 assigned.setdefault(nm, []).append(i)
         if kname in assigned:
             return None
+        # names the body computes from a dot result (directly or through others)
+        dot_fed = set()
+        for s in flat:
+            nm = _target(s)
+            if nm is not None and (any(_callee(n) == "dot" for n in ast.walk(s))
+                                   or _names_read(s) & dot_fed):
+                dot_fed.add(nm)
         uses = {}
+        acc_fed = set()
         for s in flat:
             for n in ast.walk(s):
                 if _callee(n) != "dot":
                     continue
-                for role, a in zip(("A", "B"), list(n.args)[:2]):
+                args = list(n.args)[:2]
+                for role, a in zip(("A", "B"), args):
                     nm, trans = _operand_name(a)
                     if nm is not None:
                         uses.setdefault(nm, []).append((role, trans))
+                        if role == "B" and len(args) == 2 and _names_read(args[0]) & dot_fed:
+                            acc_fed.add(nm)
         reads = {}
         for s in flat:
             for n in ast.walk(s):
@@ -283,7 +294,7 @@ class DotPipeline:
             role, trans = uses[nm][0]
             # reduction dim of the tile as loaded: A [M,K] -> 1, B [K,N] -> 0
             kdim = (1 if role == "A" else 0) ^ (1 if trans else 0)
-            staged[nm] = {"name": nm, "index": i, "kdim": kdim}
+            staged[nm] = {"name": nm, "index": i, "kdim": kdim, "acc_fed": nm in acc_fed}
         if not staged:
             return None
         # the statements computing the staged tiles' pointers and masks
@@ -719,6 +730,17 @@ class DotPipeline:
             return False
         return (R * K // epc) % self.T == 0
 
+    def _r_tile_swizzle_bit(self, info, fmt, R, K, dt):
+        """Swizzle bit of a 16-bit R-major tile: 2 when its dot will most
+        likely read it with the accumulator-ordered 16-row fragments (a B
+        operand whose A is computed from another dot's result in a
+        row-oriented kernel, with 16x16x32 MFMAs), else 3. Writer and readers
+        both take it from the record, so the guess only affects bank
+        conflicts, never results."""
+        if fmt != "r" or dt == tp.float32 or not info.get("acc_fed") or self.dot_orient() != "row":
+            return 3
+        return 2 if self.pick_instr(32, R, K, dt) == "16x16x32" else 3
+
     def _init_recs(self, state):
         recs = {}
         off = 0
@@ -748,7 +770,8 @@ class DotPipeline:
             if dma:
                 ops += R * K // epc // self.T
             recs[nm] = {"name": nm, "shape": tuple(X.shape), "dt": dt, "kdim": kdim, "R": R,
-                        "K": K, "fmt": fmt, "off": off, "dma": dma}
+                        "K": K, "fmt": fmt, "off": off, "dma": dma,
+                        "sb": self._r_tile_swizzle_bit(info, fmt, R, K, dt)}
             off += (nbytes + 15) // 16 * 16
             if V is not X:
                 V.consumed = True
@@ -794,27 +817,28 @@ class DotPipeline:
             tile = f"(({dt.ctype}*)({base} + {r['off']}))"
             full = self.mask_all_true(X.mask, X.shape) if r["dma"] else None
             if r["dma"] and full is not None and fast:
-                self._dma_stage(V, base, r["off"], fmt, R, K, dt, buffer=state.get("bufdma", False))
+                self._dma_stage(V, base, r["off"], fmt, R, K, dt, buffer=state.get("bufdma", False),
+                                sb=r["sb"])
             elif fast:
-                self._reg_stage(V, tile, fmt, R, K, dt)
+                self._reg_stage(V, tile, fmt, R, K, dt, sb=r["sb"])
             elif r["dma"] and full is not None:
                 cond = valid if full == "true" else f"{valid} && ({full})"
                 # the in-bounds copy is the hot path; the hint moves the masked
                 # register path out of the loop's straight-line code
                 self.emit(f"if (__builtin_expect({cond}, 1)) {{")
                 self.indent += 1
-                self._dma_stage(V, base, r["off"], fmt, R, K, dt)
+                self._dma_stage(V, base, r["off"], fmt, R, K, dt, sb=r["sb"])
                 self.indent -= 1
                 if full != "true":
                     self.emit(f"}} else if ({valid}) {{")
                     self.indent += 1
-                    self._reg_stage(V, tile, fmt, R, K, dt)
+                    self._reg_stage(V, tile, fmt, R, K, dt, sb=r["sb"])
                     self.indent -= 1
                 self.emit("}")
             else:
                 self.emit(f"if ({valid}) {{")
                 self.indent += 1
-                self._reg_stage(V, tile, fmt, R, K, dt)
+                self._reg_stage(V, tile, fmt, R, K, dt, sb=r["sb"])
                 self.indent -= 1
                 self.emit("}")
             for ld in (X, V):
@@ -844,7 +868,7 @@ class DotPipeline:
         conds.append(f"({' + '.join(parts) if parts else '0LL'}) < {(1 << 31) // dt.itemsize}LL")
         return " && ".join(conds)
 
-    def _dma_stage(self, X, base, boff, fmt, R, K, dt, buffer=False):
+    def _dma_stage(self, X, base, boff, fmt, R, K, dt, buffer=False, sb=3):
         """Direct-to-LDS copies of one [R, K] tile. buffer: the branch-free
         fast loop's form, a scalar descriptor on the tile's uniform start and
         a 32-bit lane offset (the entry test guarantees it fits)."""
@@ -864,7 +888,7 @@ class DotPipeline:
             elif dt == tp.float32:
                 self.emit(f"newt::LdsTileR32<{R}>::slot(_s, _k, _r);")
             else:
-                self.emit(f"newt::LdsTileR<{T}, {R}>::slot(_s, _k, _r);")
+                self.emit(f"newt::LdsTileR<{T}, {R}, {sb}>::slot(_s, _k, _r);")
             ubase = None if (off.base.is_const and off.base.const == 0) else off.base.expr
             lane = []
             for c, v in ((c0, "_r"), (c1, "_k")):
@@ -883,7 +907,7 @@ class DotPipeline:
             self.indent -= 1
             self.emit("}")
 
-    def _reg_stage(self, X, tile, fmt, R, K, dt):
+    def _reg_stage(self, X, tile, fmt, R, K, dt, sb=3):
         if fmt == "k":
             L = self.staging_layout(X)
         else:
@@ -892,10 +916,11 @@ class DotPipeline:
         r = self.emit_load(X, L)
         if r.dtype != dt:
             r = self.to_reg(r, r.layout, dt)
-        self.write_tile_to(r, tile, dt, fmt)
+        self.write_tile_to(r, tile, dt, fmt, sb)
 
-    def write_tile_to(self, r, tile, dt, fmt):
-        """Write register block r ([R, K] view) into an LDS tile of format fmt."""
+    def write_tile_to(self, r, tile, dt, fmt, sb=3):
+        """Write register block r ([R, K] view) into an LDS tile of format fmt
+        (sb: swizzle bit of a 16-bit R-major tile)."""
         L = r.layout
         R, K = L.shape
         T = dt.ctype
@@ -916,7 +941,7 @@ class DotPipeline:
             kk = self.coord(L, 1, s)
             o = (f"newt::LdsTile<{T}, {K}>::off({rr}, {kk})" if fmt == "k"
                  else f"newt::LdsTileR32<{R}>::off({kk}, {rr})" if dt == tp.float32
-                 else f"newt::LdsTileR<{T}, {R}>::off({kk}, {rr})")
+                 else f"newt::LdsTileR<{T}, {R}, {sb}>::off({kk}, {rr})")
             if chunk > 1:
                 self.emit(f"newt::store_vec<{T}, {chunk}>({tile} + {o}, {r.var} + {s});")
             else:
@@ -1070,9 +1095,13 @@ class DotPipeline:
         nks = K // KI
         orient = self.dot_orient()
         # an accumulator-layout A operand (fp16/bf16 cast of a row-per-lane dot
-        # result) is used in place, with B read in the permuted k order
-        perm = (orient == "row" and MI == 32 and isinstance(a, Reg) and isinstance(Bt, Staged)
-                and wn == 1 and a.layout == lo.mfma_c(M, K, instr, wm, 1, "row"))
+        # result) is used in place, with B read in the permuted k order: the
+        # k-slot e of a lane maps to the column its accumulator register holds
+        # (32x32: kk + 8*(e/4) + 4h + e%4 for lane half h; 16x16: kk +
+        # 16*(e/4) + 4g + e%4 for lane group g, two accumulator tiles per MFMA)
+        perm = (orient == "row" and isinstance(a, Reg) and isinstance(Bt, Staged)
+                and wn == 1 and a.layout == lo.mfma_c(M, K, instr, wm, 1, "row")
+                and (MI == 32 or os.environ.get("NEWT_PERM16", "1") != "0"))
         srcs = []
         for role, X in (("A", a), ("B", Bt)):
             if isinstance(X, Staged):
@@ -1108,14 +1137,15 @@ class DotPipeline:
                 rec, tile = X.rec, tile or tiles[idx]
                 r0 = r0 or f"{'_ra' if idx == 0 else '_rb'} + {i * MI}"
                 if rec["fmt"] == "k":
-                    fn, targs = (("lds_frag_k_perm32", f"{T}, {rec['K']}") if perm else
+                    fn, targs = ((f"lds_frag_k_perm{MI}", f"{T}, {rec['K']}") if perm else
                                  ("lds_frag_k", f"{T}, {rec['K']}, {MI}"))
                 else:
-                    fn, targs = (("lds_frag_r_perm32", f"{T}, {rec['R']}") if perm else
-                                 ("lds_frag_r", f"{T}, {rec['R']}, {MI}"))
+                    fn, targs = ((f"lds_frag_r_perm{MI}", f"{T}, {rec['R']}, {rec['sb']}") if perm
+                                 else ("lds_frag_r", f"{T}, {rec['R']}, {MI}, {rec['sb']}"))
                 return f"newt::{fn}<{targs}>({tile}, {r0}, {kk}, _lane)"
             if kind == "acc":
-                slots = [self._slot_for(X.layout, {0: i * MI, 1: kk + 8 * (e // 4) + (e % 4)})
+                step = 8 if MI == 32 else 16
+                slots = [self._slot_for(X.layout, {0: i * MI, 1: kk + step * (e // 4) + (e % 4)})
                          for e in range(8)]
             else:
                 slots = [self._slot_for(X.layout, {0: i * MI, 1: kk + e}) for e in range(8)]

@@ -412,16 +412,20 @@ __host__ __device__ __forceinline__ void lds_tile_slot(int slot, int& r, int& k)
 //   32-row instructions: 4 consecutive k-rows x 32 rows (two units each);
 //   16-row instructions: k-rows kk..kk+3 and kk+8..kk+11 x 16 rows.
 // k % 4 picks the 64-byte quarter (rows of >= 256 bytes; shorter rows already
-// place consecutive k-rows in different quarters) and bit 3 of k the 32-byte
-// half of the quarter.
+// place consecutive k-rows in different quarters) and bit SB of k the 32-byte
+// half of the quarter. SB = 3 serves the 16-row fragments above; SB = 2 serves
+// the 16-row fragments in the permuted accumulator order (lds_frag_r_perm16),
+// whose 32 lanes read k-rows kk..kk+7. 32-row fragments are conflict-free
+// under either.
 // ---------------------------------------------------------------------------
-template <typename T, int RD>
+template <typename T, int RD, int SB = 3>
 struct LdsTileR {
   static_assert(sizeof(T) == 2 && RD >= 32 && RD % 32 == 0, "R-major tiles hold >= 32 16-bit rows");
+  static_assert(SB == 2 || SB == 3, "swizzle bit is 2 or 3");
   static constexpr int ROW_BYTES = RD * 2;
   static constexpr int LOG_ROWS_PER_256 = ROW_BYTES >= 256 ? 0 : (ROW_BYTES == 128 ? 1 : 2);
   __host__ __device__ __forceinline__ static int swz(int k) {
-    return (((k & 3) >> LOG_ROWS_PER_256) << 1) | ((k >> 3) & 1);
+    return (((k & 3) >> LOG_ROWS_PER_256) << 1) | ((k >> SB) & 1);
   }
   __host__ __device__ __forceinline__ static int off(int k, int r) {
     return k * RD + (((r >> 4) ^ swz(k)) << 4) + (r & 15);
@@ -466,9 +470,9 @@ __host__ __device__ __forceinline__ void frag_r_coords(int r0, int kk, int lane,
   kr = kk + 8 * (lane / MI) + (i >> 2);
 }
 
-template <typename T, int RD, int MI>
+template <typename T, int RD, int MI, int SB = 3>
 __device__ __forceinline__ i16x8 lds_frag_r(const T* tile, int r0, int kk, int lane) {
-  typedef LdsTileR<T, RD> L;
+  typedef LdsTileR<T, RD, SB> L;
   int kr, cb;
   frag_r_coords<MI>(r0, kk, lane, kr, cb);
   const __attribute__((address_space(3))) char* b =
@@ -490,15 +494,38 @@ __host__ __device__ __forceinline__ void frag_r_perm32_coords(int r0, int kk, in
   kr = kk + 4 * (lane >> 5) + (i >> 2);
 }
 
-template <typename T, int RD>
+template <typename T, int RD, int SB = 3>
 __device__ __forceinline__ i16x8 lds_frag_r_perm32(const T* tile, int r0, int kk, int lane) {
-  typedef LdsTileR<T, RD> L;
+  typedef LdsTileR<T, RD, SB> L;
   int kr, cb;
   frag_r_perm32_coords(r0, kk, lane, kr, cb);
   const __attribute__((address_space(3))) char* b =
       (const __attribute__((address_space(3))) char*)tile;
   i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(b + 2 * L::off(kr, cb)));
   i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(b + 2 * L::off(kr + 8, cb)));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// The same for a 16x16 MFMA accumulator, whose lane group g = l / 16 holds
+// columns 4g..4g+3 of each 16: element e of lane group g is
+// k = kk + 16*(e/4) + 4g + e%4, so one 16x16x32 MFMA contracts the columns of
+// two adjacent accumulator tiles.
+__host__ __device__ __forceinline__ void frag_r_perm16_coords(int r0, int kk, int lane, int& kr,
+                                                              int& cb) {
+  const int i = lane & 15;
+  cb = r0 + 4 * (i & 3);
+  kr = kk + 4 * (lane >> 4) + (i >> 2);
+}
+
+template <typename T, int RD, int SB = 2>
+__device__ __forceinline__ i16x8 lds_frag_r_perm16(const T* tile, int r0, int kk, int lane) {
+  typedef LdsTileR<T, RD, SB> L;
+  int kr, cb;
+  frag_r_perm16_coords(r0, kk, lane, kr, cb);
+  const __attribute__((address_space(3))) char* b =
+      (const __attribute__((address_space(3))) char*)tile;
+  i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(b + 2 * L::off(kr, cb)));
+  i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(b + 2 * L::off(kr + 16, cb)));
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
@@ -591,6 +618,18 @@ __device__ __forceinline__ i16x8 lds_frag_k_perm32(const T* tile, int r0, int kk
   const int k = kk + 4 * (lane >> 5);
   i16x4 lo = *(const i16x4*)(tile + L::off(r, k));
   i16x4 hi = *(const i16x4*)(tile + L::off(r, k + 8));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// K-major tile fragment in the permuted 16x16 accumulator k order (see
+// lds_frag_r_perm16): two 8-byte reads per lane.
+template <typename T, int KD>
+__device__ __forceinline__ i16x8 lds_frag_k_perm16(const T* tile, int r0, int kk, int lane) {
+  typedef LdsTile<T, KD> L;
+  const int r = r0 + (lane & 15);
+  const int k = kk + 4 * (lane >> 4);
+  i16x4 lo = *(const i16x4*)(tile + L::off(r, k));
+  i16x4 hi = *(const i16x4*)(tile + L::off(r, k + 16));
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 

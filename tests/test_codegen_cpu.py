@@ -538,6 +538,50 @@ def test_loaded_block_keeps_its_layout_against_a_broadcast_statistic():
     assert "store_vec<float, 4>" in src
 
 
+def test_chained_dots_detected():
+    """Kernels that feed one dot's result into another (attention's P @ V)
+    are found on the AST; a matmul's accumulator chain and dot-free kernels
+    are not."""
+    from newt_amd.compiler import _chained_dots as chained
+    f = lambda k: fndef_of(k)[0]
+    assert chained(f(W.attention_kernel)) and chained(f(W.attention_plain_kernel))
+    for k in (W.matmul_kernel, W.softmax_kernel, W.layernorm_kernel, W.add_kernel):
+        assert not chained(f(k))
+
+    def two_step(a_ptr, b_ptr, c_ptr, o_ptr, B: nl.constexpr):
+        r = nl.arange(0, B)
+        a = nl.load(a_ptr + r[:, None] * B + r[None, :])
+        b = nl.load(b_ptr + r[:, None] * B + r[None, :])
+        c = nl.load(c_ptr + r[:, None] * B + r[None, :])
+        t = nl.dot(a, b)
+        u = t.to(nl.float16)
+        nl.store(o_ptr + r[:, None] * B + r[None, :], nl.dot(u, c))
+
+    assert chained(f(two_step))
+
+
+@pytest.mark.parametrize("mode,instr,fn", [("", "16x16x32", "lds_frag_r_perm16"),
+                                            ("32", "32x32x16", "lds_frag_r_perm32")])
+def test_attention_p_feeds_pv_from_registers(monkeypatch, mode, instr, fn):
+    """Both attention forms run both dots on 16x16x32 MFMAs by default (on
+    32x32x16 with NEWT_MFMA=32): the bf16 cast of the score accumulator is the
+    P @ V dot's A operand in place, with V read from LDS in the permuted k
+    order, so no block goes through an LDS layout conversion. The V tile takes
+    the swizzle its 16-row reader needs."""
+    monkeypatch.setenv("NEWT_MFMA", mode)
+    args = _attention_args()
+    for kern in (W.attention_kernel, W.attention_plain_kernel):
+        for D in (64, 128):
+            for causal in (False, True):
+                src, _ = compile_source(kern, args, {"BLOCK_M": 256, "BLOCK_N": 64, "D": D,
+                                                     "CAUSAL": causal},
+                                        num_warps=8, num_stages=2, waves_per_eu=2)
+                assert f"newt::mfma_{instr}" in src
+                assert f"newt::{fn}<__bf16, {D}, {2 if mode == '' else 3}>" in src
+                assert "_cv" not in src
+                assert f"LdsTileR<__bf16, {D}, {2 if mode == '' else 3}>" in src
+
+
 def test_attention_program_ids_not_grouped():
     args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
     args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})

@@ -19,7 +19,10 @@ this checks
     (r >> 2) & 3 key 2-way). A ds_read_b64_tr_b16 serves 32 consecutive
     lanes per cycle, consistent with its four measured patterns (16-row
     fragments 2-way under a 64-byte-granular swizzle, 0 under the current
-    one; 32-row fragments 0 under both).
+    one; 32-row fragments 0 under both). R-major tiles take the swizzle bit
+    of k their 16-row reader needs (3 for plain fragments, 2 for the
+    accumulator-ordered ones); the check also shows each reader 2-way under
+    the other bit.
 """
 
 import os
@@ -52,11 +55,12 @@ static int degree(const std::vector<std::pair<int, int>>& acc) {
   return d;
 }
 
-// R-major [KD][RD] tile read by the transposed fragment reader of an MI-row
-// instruction (PERM: the 32x32 accumulator-ordered variant)
-template <int RD, int KD, int MI, bool PERM>
+// R-major [KD][RD] tile (swizzle bit SB) read by the transposed fragment
+// reader of an MI-row instruction (PERM: the accumulator-ordered variant of
+// that instruction)
+template <int RD, int KD, int MI, bool PERM, int SB = 3>
 void check_r() {
-  typedef LdsTileR<f16, RD> L;
+  typedef LdsTileR<f16, RD, SB> L;
   std::vector<int> seen(KD * RD, 0);
   bool ok = true;
   for (int k = 0; k < KD; k++)
@@ -78,14 +82,15 @@ void check_r() {
           std::vector<std::pair<int, int>> acc;
           for (int l = 32 * g; l < 32 * g + 32; l++) {
             int kr, cb;
-            if (PERM) frag_r_perm32_coords(r0, kk, l, kr, cb);
+            if (PERM && MI == 32) frag_r_perm32_coords(r0, kk, l, kr, cb);
+            else if (PERM) frag_r_perm16_coords(r0, kk, l, kr, cb);
             else frag_r_coords<MI>(r0, kk, l, kr, cb);
-            kr += second * (PERM ? 8 : 4);
+            kr += second * (PERM ? (MI == 32 ? 8 : 16) : 4);
             acc.push_back({2 * L::off(kr, cb), 8});
           }
           worst = std::max(worst, degree(acc));
         }
-  printf("R %d %d %d %d %d %d\n", RD, KD, MI, (int)PERM, (int)ok, worst);
+  printf("R %d %d %d %d %d %d %d\n", RD, KD, MI, (int)PERM, SB, (int)ok, worst);
 }
 
 // fp32 R-major [KD][RD] tile read four floats per lane in the permuted k order
@@ -160,6 +165,12 @@ int main() {
   check_r<256, 64, 32, false>(); check_r<256, 128, 16, false>();
   check_r<64, 64, 32, true>();   check_r<128, 64, 32, true>();
   check_r<128, 128, 32, true>();
+  check_r<32, 32, 16, true, 2>();  check_r<64, 64, 16, true, 2>();
+  check_r<128, 64, 16, true, 2>(); check_r<128, 128, 16, true, 2>();
+  check_r<256, 64, 16, true, 2>();
+  check_r<64, 64, 32, false, 2>(); check_r<128, 64, 32, false, 2>();
+  check_r<128, 64, 32, true, 2>(); check_r<256, 32, 32, false, 2>();
+  check_r<128, 64, 16, true, 3>(); check_r<128, 64, 16, false, 2>();
   check_r32<64, 16>(); check_r32<128, 16>(); check_r32<256, 32>();
   check_k<32, 32>();  check_k<32, 16>();
   check_k<64, 32>();  check_k<64, 16>();
@@ -187,10 +198,12 @@ def layout_report(tmp_path_factory):
 
 def test_r_major_tiles_are_bijective_and_conflict_free(layout_report):
     r = {k: v for k, v in layout_report.items() if k[0] == "R"}
-    assert len(r) == 13
+    assert len(r) == 24
+    # (RD, KD, MI, PERM, SB): the two reads each swizzle bit is not for
+    mismatched = {(128, 64, 16, 1, 3), (128, 64, 16, 0, 2)}
     for key, (ok, worst) in r.items():
         assert ok == 1, key
-        assert worst == 1, key
+        assert worst == (2 if key[1:] in mismatched else 1), key
 
 
 def test_fp32_r_major_tiles_are_bijective_and_conflict_free(layout_report):
