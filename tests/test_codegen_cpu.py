@@ -582,6 +582,47 @@ def test_attention_p_feeds_pv_from_registers(monkeypatch, mode, instr, fn):
                 assert f"LdsTileR<__bf16, {D}, {2 if mode == '' else 3}>" in src
 
 
+def _chained_dots_kernel(a_ptr, k_ptr, v_ptr, o_ptr, s_ptr, N, svn, svd,
+                         BLOCK_M: nl.constexpr, BLOCK_N: nl.constexpr, D: nl.constexpr):
+    pid = nl.program_id(0)
+    offs_m = pid * BLOCK_M + nl.arange(0, BLOCK_M)
+    offs_d = nl.arange(0, D)
+    a = nl.load(a_ptr + offs_m[:, None] * D + offs_d[None, :])
+    acc = nl.zeros((BLOCK_M, D), dtype=nl.float32)
+    rs = nl.zeros((BLOCK_M,), dtype=nl.float32)
+    for start_n in range(0, N, BLOCK_N):
+        offs_n = start_n + nl.arange(0, BLOCK_N)
+        k = nl.load(k_ptr + offs_n[:, None] * D + offs_d[None, :])
+        s = nl.dot(a, nl.trans(k))
+        rs = rs + nl.sum(s, axis=1)
+        v = nl.load(v_ptr + offs_n[:, None] * svn + offs_d[None, :] * svd)
+        acc = nl.dot(s.to(nl.float16), v, acc)
+    nl.store(o_ptr + offs_m[:, None] * D + offs_d[None, :], acc)
+    nl.store(s_ptr + offs_m, rs)
+
+
+@pytest.mark.parametrize("mode,instr", [("", "16x16x32"), ("32", "32x32x16")])
+@pytest.mark.parametrize("v_keys_contiguous", [False, True])
+def test_chained_dot_reads_v_in_accumulator_order(monkeypatch, mode, instr, v_keys_contiguous):
+    """The kernel of tests/test_gpu_pipeline_dot.py::test_dot_result_feeds_next_dot
+    takes the permuted reader of its V tile's format and instruction: R-major
+    (rows contiguous; swizzle bit 2 at 16x16x32) or K-major (keys
+    contiguous), and converts nothing through LDS."""
+    monkeypatch.setenv("NEWT_MFMA", mode)
+    args = {"a_ptr": (F16P, A16), "k_ptr": (F16P, A16), "v_ptr": (F16P, A16),
+            "o_ptr": (F32P, A16), "s_ptr": (F32P, A16), "N": (tp.int32, D16)}
+    one = (tp.int32, {"eq1": True})
+    args["svn"], args["svd"] = (one, (tp.int32, D16)) if v_keys_contiguous else ((tp.int32, D16), one)
+    src, _ = compile_source(_chained_dots_kernel, args, {"BLOCK_M": 128, "BLOCK_N": 64, "D": 64},
+                            num_warps=4, num_stages=2)
+    mi = instr.split("x")[0]
+    want = (f"lds_frag_k_perm{mi}<_Float16, 64>" if v_keys_contiguous else
+            f"lds_frag_r_perm{mi}<_Float16, 64, {2 if mi == '16' else 3}>")
+    assert f"newt::{want}" in src
+    assert f"newt::mfma_{instr}" in src
+    assert "_cv" not in src
+
+
 def test_attention_program_ids_not_grouped():
     args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
     args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})

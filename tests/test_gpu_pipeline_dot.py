@@ -225,3 +225,51 @@ def kloop_k2(a_ptr, b_ptr, o_ptr, K, sam, BM: nl.constexpr, BN: nl.constexpr, BK
         pa += BK
         pb += BK * BN
     nl.store(o_ptr + rm[:, None] * BN + rn[None, :], acc)
+
+
+@newt.jit
+def chained_dots_k(a_ptr, k_ptr, v_ptr, o_ptr, s_ptr, N, svn, svd,
+                   BLOCK_M: nl.constexpr, BLOCK_N: nl.constexpr, D: nl.constexpr):
+    pid = nl.program_id(0)
+    offs_m = pid * BLOCK_M + nl.arange(0, BLOCK_M)
+    offs_d = nl.arange(0, D)
+    a = nl.load(a_ptr + offs_m[:, None] * D + offs_d[None, :])
+    acc = nl.zeros((BLOCK_M, D), dtype=nl.float32)
+    rs = nl.zeros((BLOCK_M,), dtype=nl.float32)
+    for start_n in range(0, N, BLOCK_N):
+        offs_n = start_n + nl.arange(0, BLOCK_N)
+        k = nl.load(k_ptr + offs_n[:, None] * D + offs_d[None, :])
+        s = nl.dot(a, nl.trans(k))
+        rs = rs + nl.sum(s, axis=1)
+        v = nl.load(v_ptr + offs_n[:, None] * svn + offs_d[None, :] * svd)
+        acc = nl.dot(s.to(nl.float16), v, acc)
+    nl.store(o_ptr + offs_m[:, None] * D + offs_d[None, :], acc)
+    nl.store(s_ptr + offs_m, rs)
+
+
+@pytest.mark.parametrize("mfma", ["", "32"])
+@pytest.mark.parametrize("v_keys_contiguous", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+def test_dot_result_feeds_next_dot(mfma, v_keys_contiguous, D, monkeypatch):
+    """A dot's fp16 result as the next dot's A operand inside a pipelined loop
+    (attention's P @ V without the softmax). The accumulator registers feed
+    the second MFMA in place, and V is read from LDS in the matching permuted
+    key order: row-major V (an R-major tile, swizzled for that read) or V
+    stored keys-contiguous (a K-major tile). Both on 16x16x32 MFMAs (the
+    default for such kernels) and on 32x32x16 (NEWT_MFMA=32). Checked against
+    torch in fp32 on the fp16 rounding of the first product; a key order that
+    pairs P and V wrongly gives an error of order 1."""
+    monkeypatch.setenv("NEWT_MFMA", mfma)
+    M, N, BM, BN = 256, 512, 128, 64
+    a, k, v = rnd((M, D), torch.float16, 1), rnd((N, D), torch.float16, 2), rnd((N, D), torch.float16, 3)
+    vbuf, svn, svd = (v.t().contiguous(), 1, N) if v_keys_contiguous else (v, D, 1)
+    o = torch.empty(M, D, device="cuda", dtype=torch.float32)
+    s = torch.empty(M, device="cuda", dtype=torch.float32)
+    print(f"chained dots: D={D} V keys-contiguous={v_keys_contiguous} NEWT_MFMA={mfma!r}", flush=True)
+    chained_dots_k[(M // BM,)](a, k, vbuf, o, s, N, svn, svd, BLOCK_M=BM, BLOCK_N=BN, D=D,
+                               num_warps=4, num_stages=2)
+    s32 = a.float() @ k.float().t()
+    want_o = s32.half().float() @ v.float()
+    rel = ((o - want_o).norm() / want_o.norm()).item()
+    assert rel < 2e-3, rel
+    torch.testing.assert_close(s, s32.sum(1), rtol=1e-4, atol=1e-3)
