@@ -24,7 +24,7 @@ SWITCHES = [
     ("NEWT_PID_GROUP", "0"), ("NEWT_PID_GROUP", "2"), ("NEWT_BARE_BARRIER", "1"),
     ("NEWT_WHERE_VERSION", "0"), ("NEWT_NT_LOAD", "1"), ("NEWT_NT_STREAM", "1"),
     ("NEWT_REDUCE_PINGPONG", "0"), ("NEWT_PIPE_CLAMP", "0"), ("NEWT_CSE", "0"),
-    ("NEWT_VERSION_BODY", "0"), ("NEWT_PID_LPT", "0"),
+    ("NEWT_VERSION_BODY", "0"), ("NEWT_PID_LPT", "0"), ("NEWT_PERM16", "0"),
 ]
 
 
