@@ -8,7 +8,9 @@ Lowering (this backend's own): the reduced dimension's logical bits are split
 by the hardware index that carries them in the operand's layout -
   register bits -> combined in-thread,
   lane bits     -> wave64 butterfly (newt::lane_reduce: DPP quad_perm for
-                   xor 1/2, ds_swizzle for xor 4..16, ds_bpermute for xor 32),
+                   xor 1/2, DPP row mirrors (or ds_swizzle) for xor 4/8,
+                   v_permlane16/32_swap for xor 16/32; newt::lane_reduce2
+                   reduces two results held by the same lanes at once),
   wave bits     -> one LDS exchange + barrier.
 Replicated hardware bits are never combined (they hold copies). The result of
 an axis reduction keeps the operand's layout minus the reduced bits, so a row
@@ -133,9 +135,15 @@ class ReduceOps:
                 self.emit(f"{out.at(t)} = {self._combine(op, out.at(t), e)};")
         lmask = sum(1 << i for i, b in enumerate(L.lane) if b is not None and b[0] == axis)
         if lmask:
-            for t in range(Lr.nslots):
-                if not Lr.slot_is_canonical(t):
-                    continue
+            slots = [t for t in range(Lr.nslots) if Lr.slot_is_canonical(t)]
+            # results held two or more to a lane (a 16x16 MFMA tile's rows)
+            # share the permlane steps of lane bits 4 and 5 in pairs
+            if lmask & 48 and os.environ.get("NEWT_PAIR_REDUCE", "1") != "0":
+                while len(slots) >= 2:
+                    t0, t1 = slots.pop(0), slots.pop(0)
+                    self.emit(f"newt::lane_reduce2<{_OPS[op]}, {lmask}>({out.at(t0)}, "
+                              f"{out.at(t1)});")
+            for t in slots:
                 self.emit(f"{out.at(t)} = newt::lane_reduce<{_OPS[op]}, {lmask}>({out.at(t)});")
         wbits = [i for i, b in enumerate(L.wave) if b is not None and b[0] == axis]
         if wbits:

@@ -197,20 +197,27 @@ __device__ __forceinline__ int mirror_lane_i32(int v) {
 // from one v_permlane{16,32}_swap: swapping the odd rows (M = 16) or the upper
 // half (M = 32) of one copy of v with the even rows / lower half of another
 // leaves v[l & ~M] in the first copy and v[l | M] in the second.
+// With two different values a and b, the same swap leaves x = a[l] where bit
+// M of l is clear and b[l & ~M] where it is set, and y = a[l | M] / b[l].
 template <int M>
-__device__ __forceinline__ void pair_lanes_i32(int v, int& lo, int& hi) {
+__device__ __forceinline__ void swap_lanes_i32(int a, int b, int& x, int& y) {
   static_assert(M == 16 || M == 32, "pair mask");
   if constexpr (M == 16) {
-    auto r = __builtin_amdgcn_permlane16_swap((u32)v, (u32)v, false, false);
-    u32 a = r[0], b = r[1];
-    lo = (int)a;
-    hi = (int)b;
+    auto r = __builtin_amdgcn_permlane16_swap((u32)a, (u32)b, false, false);
+    u32 p = r[0], q = r[1];
+    x = (int)p;
+    y = (int)q;
   } else {
-    auto r = __builtin_amdgcn_permlane32_swap((u32)v, (u32)v, false, false);
-    u32 a = r[0], b = r[1];
-    lo = (int)a;
-    hi = (int)b;
+    auto r = __builtin_amdgcn_permlane32_swap((u32)a, (u32)b, false, false);
+    u32 p = r[0], q = r[1];
+    x = (int)p;
+    y = (int)q;
   }
+}
+
+template <int M>
+__device__ __forceinline__ void pair_lanes_i32(int v, int& lo, int& hi) {
+  swap_lanes_i32<M>(v, v, lo, hi);
 }
 
 template <int W, typename T>
@@ -253,6 +260,32 @@ __device__ __forceinline__ void pair_lanes(T v, T& lo, T& hi) {
   }
 }
 
+template <int M, typename T>
+__device__ __forceinline__ void swap_lanes(T a, T b, T& x, T& y) {
+  if constexpr (sizeof(T) == 4) {
+    int p, q;
+    swap_lanes_i32<M>(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), p, q);
+    x = __builtin_bit_cast(T, p);
+    y = __builtin_bit_cast(T, q);
+  } else if constexpr (sizeof(T) == 8) {
+    u32x2 wa = __builtin_bit_cast(u32x2, a), wb = __builtin_bit_cast(u32x2, b), x2, y2;
+    int p, q;
+    swap_lanes_i32<M>((int)wa.x, (int)wb.x, p, q);
+    x2.x = (u32)p;
+    y2.x = (u32)q;
+    swap_lanes_i32<M>((int)wa.y, (int)wb.y, p, q);
+    x2.y = (u32)p;
+    y2.y = (u32)q;
+    x = __builtin_bit_cast(T, x2);
+    y = __builtin_bit_cast(T, y2);
+  } else {
+    int p, q;
+    swap_lanes_i32<M>((int)a, (int)b, p, q);
+    x = (T)p;
+    y = (T)q;
+  }
+}
+
 // Butterfly over the lane bits set in MASK (compile-time), combining with Op,
 // every step on the VALU (no LDS-pipe swizzle or bpermute) where it can be:
 //   bits 0, 1: DPP quad_perm (the xor partner);
@@ -281,6 +314,35 @@ __device__ __forceinline__ T lane_reduce(T v) {
     v = Op::op(lo, hi);
   }
   return v;
+}
+
+// Two values reduced over the same lane bits, as two lane_reduce calls would,
+// with the permlane steps shared (MASK has bit 4 or 5; M1 is 16 when it has
+// bit 4, else 32). After the bits below 16 are reduced in each value, one
+// swap between a and b combines a's lane pairs where bit M1 of the lane is
+// clear and b's where it is set; with both bits, a second step reduces bit 5
+// of that mix; one more swap hands every lane both results. Every combine
+// takes the lower lane's value first, as lane_reduce does, so the results are
+// bit-identical to two lane_reduce calls. Over bits 4 and 5 it issues 3 swaps
+// and 2 combines where the two calls issue 4 and 4.
+template <typename Op, int MASK, typename T>
+__device__ __forceinline__ void lane_reduce2(T& a, T& b) {
+  static_assert((MASK & 48) != 0, "lane_reduce2 shares the steps of lane bits 4 and 5");
+  constexpr int LOW = MASK & 15;
+  constexpr int M1 = (MASK & 16) ? 16 : 32;
+  if constexpr (LOW != 0) {
+    a = lane_reduce<Op, LOW>(a);
+    b = lane_reduce<Op, LOW>(b);
+  }
+  T x, y;
+  swap_lanes<M1>(a, b, x, y);
+  T c = Op::op(x, y);
+  if constexpr (M1 == 16 && (MASK & 32)) {
+    T lo, hi;
+    pair_lanes<32>(c, lo, hi);
+    c = Op::op(lo, hi);
+  }
+  pair_lanes<M1>(c, a, b);
 }
 
 // ---------------------------------------------------------------------------

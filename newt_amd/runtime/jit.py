@@ -43,7 +43,8 @@ _CODEGEN_ENV = ("NEWT_VEC", "NEWT_PIPELINE_DOT", "NEWT_LDS_DMA", "NEWT_MFMA", "N
                 "NEWT_PIPE_VERSION", "NEWT_PLR", "NEWT_SCHED", "NEWT_HOIST_LOADS", "NEWT_PID_GROUP", "NEWT_IGLP",
                 "NEWT_BUFFER_DMA", "NEWT_NT_STORE", "NEWT_BARE_BARRIER", "NEWT_WHERE_VERSION", "NEWT_NT_LOAD", "NEWT_NT_STREAM",
                 "NEWT_REDUCE_PINGPONG", "NEWT_PIPE_CLAMP", "NEWT_CSE", "NEWT_VERSION_BODY",
-                "NEWT_PID_LPT", "NEWT_PERM16")
+                "NEWT_PID_LPT", "NEWT_PERM16",
+                "NEWT_PAIR_REDUCE")
 _CODEGEN_ENV_B = tuple(k.encode() for k in _CODEGEN_ENV)
 
 

@@ -12,6 +12,8 @@ layout switches, softmax and layernorm rows.
 import pytest
 import torch
 
+import newt_amd as newt
+import newt_amd.language as nl
 from oracle import newt_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -25,6 +27,7 @@ SWITCHES = [
     ("NEWT_WHERE_VERSION", "0"), ("NEWT_NT_LOAD", "1"), ("NEWT_NT_STREAM", "1"),
     ("NEWT_REDUCE_PINGPONG", "0"), ("NEWT_PIPE_CLAMP", "0"), ("NEWT_CSE", "0"),
     ("NEWT_VERSION_BODY", "0"), ("NEWT_PID_LPT", "0"), ("NEWT_PERM16", "0"),
+    ("NEWT_PAIR_REDUCE", "0"),
 ]
 
 
@@ -93,3 +96,79 @@ def test_heaviest_first_order_is_bit_identical(monkeypatch, B, H, S):
     ref = orc.attention(npf(q), npf(k), npf(v), 128 ** -0.5, True, p_dtype="bfloat16",
                         out_dtype="bfloat16")
     assert orc.rel_frobenius(npf(outs[0]), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("tile", ["16x16, 32 rows per wave", "32x32, 64 rows per wave"])
+@pytest.mark.parametrize("plain", [False, True])
+@pytest.mark.parametrize("causal", [False, True])
+def test_paired_lane_reduce_is_bit_identical(monkeypatch, causal, plain, tile):
+    """Attention's row statistics with two rows per lane run as
+    newt::lane_reduce2 pairs: on the default 16x16x32 accumulator (rows
+    reduced over lane bits 4 and 5) and on 32x32x16 with 64 rows per wave
+    (lane bit 5 alone). A pair makes the same combines in the same operand
+    order as one lane_reduce per row (NEWT_PAIR_REDUCE=0): the outputs are
+    equal bit for bit, and match the oracle."""
+    from newt_amd import workloads as W
+    print(f"attention causal={causal} plain={plain} {tile} NEWT_PAIR_REDUCE on/off", flush=True)
+    D = 128 if tile.startswith("16") else 64
+    kw = {} if tile.startswith("16") else {"BLOCK_M": 128, "num_warps": 2}
+    if not tile.startswith("16"):
+        monkeypatch.setenv("NEWT_MFMA", "32")
+    q, k, v = (seeded((2, 4, 700, D), s, dtype=torch.bfloat16) for s in (64, 65, 66))
+    outs = []
+    for pair in ("1", "0"):
+        monkeypatch.setenv("NEWT_PAIR_REDUCE", pair)
+        o = torch.full_like(q, float("nan"))
+        W.attention(q, k, v, causal=causal, out=o, plain=plain, **kw)
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    assert orc.rel_frobenius(npf(outs[0]), ref) <= 1e-2
+
+
+@newt.jit
+def rowred(x_ptr, s_ptr, mx_ptr, mn_ptr, RB: nl.constexpr, CB: nl.constexpr):
+    r = nl.arange(0, RB)
+    c = nl.arange(0, CB)
+    x = nl.load(x_ptr + r[:, None] * CB + c[None, :])
+    nl.store(s_ptr + r, nl.sum(x, axis=1))
+    nl.store(mx_ptr + r, nl.max(x, axis=1))
+    nl.store(mn_ptr + r, nl.min(x, axis=1))
+
+
+@pytest.mark.parametrize("R,C,warps", [(8, 1024, 1), (4, 256, 1), (16, 512, 2), (6, 128, 1),
+                                        (2, 2048, 1)])
+def test_paired_row_reductions(monkeypatch, R, C, warps):
+    """Row sums, maxima and minima of blocks whose rows are spread over 32 or
+    64 lanes with several rows per lane (their results pair up in
+    newt::lane_reduce2, after the lane bits below 16): int32 results equal
+    torch's exactly; float results (with signed zeros, infinities and NaNs
+    in the rows) equal those of one lane_reduce per row bit for bit."""
+    print(f"row reductions [{R},{C}] on {warps} waves", flush=True)
+    RB = 1 << (R - 1).bit_length()
+    g = torch.Generator().manual_seed(R * C)
+    xi = torch.randint(-1000, 1000, (RB, C), generator=g, dtype=torch.int32).cuda()
+    xf = (torch.randn(RB, C, generator=g) * 3).cuda()
+    xf[0, 5], xf[1, 7], xf[1 % RB, 9] = float("-inf"), float("nan"), -0.0
+    xf[2 % RB, :] = -0.0
+    xf[3 % RB, 3] = float("inf")
+    res = {}
+    for pair in ("1", "0"):
+        monkeypatch.setenv("NEWT_PAIR_REDUCE", pair)
+        for name, x in (("i", xi), ("f", xf)):
+            outs = [torch.empty(RB, device="cuda", dtype=x.dtype) for _ in range(3)]
+            rowred[(1,)](x, *outs, RB=RB, CB=C, num_warps=warps)
+            res[(pair, name)] = outs
+    torch.cuda.synchronize()
+    s, mx, mn = res[("1", "i")]
+    assert torch.equal(s, xi.sum(1, dtype=torch.int32))
+    assert torch.equal(mx, xi.max(1).values) and torch.equal(mn, xi.min(1).values)
+    for a, b in zip(res[("1", "f")], res[("0", "f")]):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    finite = torch.isfinite(xf).all(1)
+    ref = xf[finite].double().sum(1).float()
+    torch.testing.assert_close(res[("1", "f")][0][finite], ref, rtol=1e-5, atol=1e-3)
+    assert torch.equal(res[("1", "f")][1][finite], xf[finite].max(1).values)
+    assert torch.equal(res[("1", "f")][2][finite], xf[finite].min(1).values)
