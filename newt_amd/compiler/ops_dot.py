@@ -6,9 +6,11 @@ M, N multiples of 16; K a multiple of 16 (fp16/bf16) or 8 (fp32); `acc`
 accumulates; a dot-consumed load used again after a flush point is an error.
 
 Lowering (this backend's own):
-  * instruction: v_mfma_f32_32x32x16_{f16,bf16} when both M and N split into
-    32-wide tiles, else 16x16x32 (K % 32 == 0) or 16x16x16; fp32 uses
-    v_mfma_f32_32x32x2f32 / 16x16x4f32 (full fp32, no tf32 truncation);
+  * instruction: v_mfma_f32_16x16x32_{f16,bf16} or 32x32x16 by the kernel's
+    shape (DotOps.pick_instr: 16x16x32 for kernels of at most 4 waves and for
+    chained row-oriented dots), 16x16x16 when K % 32 != 0 and the tiles are
+    not 32-wide; fp32 uses v_mfma_f32_32x32x2f32 / 16x16x4f32 (full fp32, no
+    tf32 truncation);
   * orientation: in kernels that reduce rows (softmax-style statistics of a
     dot result) the MFMA computes C^T = B^T A^T so each lane owns one ROW of
     the result and row statistics stay in-lane; elsewhere it computes C = A B
@@ -93,13 +95,19 @@ class DotOps:
         return M, N, K, dt, instr, wm, wn, rep
 
     def pick_instr(self, M, N, K, dt):
-        """32x32x16, except
-        - for a column-oriented dot whose waves each hold a tile of at least
-          128x128 over a single 32-deep k-step: there the 16x16x32 MFMA (same
-          rate, half the latency) measured ~3.5% faster for the 4-wave
-          256x256x32 matmul, while it is slower with more waves per SIMD
-          (their latency is already hidden) or with deeper k-steps (register
-          pressure);
+        """32x32x16, except for 16x16x32 (same rate, half the latency, half the
+        accumulator registers read and written per flop)
+        - for a column-oriented dot in a kernel of at most 4 waves (one wave
+          per SIMD per workgroup), whose MFMA latency no second wave of the
+          workgroup hides. Measured against 32x32x16, one box, back-to-back
+          windows: the 4-wave 256x256x32 matmul tile +3.5%; 2048^3 on the
+          128x128x64 4-stage tile +1.2% fp16 and +5-7.5% bf16, other 4-wave
+          2048^3 tiles +0.6-1.2%; 1024^3 on 64x64x64 +4-5% with 4 stages, -3%
+          with 3 (the autotuner chooses between them);
+        - for a column-oriented dot of more waves whose waves each hold a tile
+          of at least 128x128 over a single 32-deep k-step (8-wave tiles
+          below that ran 2.5-27% slower on 16x16x32: 256x128x32, 256x256x32,
+          256x256x64 at 4096^3);
         - for every dot of a row-oriented kernel that feeds one dot's result
           into another (flash attention): 16x16x32, whose accumulator feeds
           the next MFMA from registers as 32x32x16's does. At the package
@@ -109,9 +117,13 @@ class DotOps:
         NEWT_MFMA=16 / 32 forces the shape wherever it fits."""
         instr = _choose_instr(M, N, K, dt)
         mode = os.environ.get("NEWT_MFMA", "")
-        if self.prefer_rows or instr != "32x32x16" or K != 32:
+        if self.prefer_rows or instr != "32x32x16":
             small = mode == "16" or (self.prefer_rows and self.chained_dots and mode != "32")
             return _choose_instr(M, N, K, dt, small_first=small)
+        if mode or self.W <= 4:
+            return _choose_instr(M, N, K, dt, small_first=mode != "32")
+        if K != 32:
+            return instr
         wm, wn, _ = self.wave_grid(M, N, instr)
         big = M // wm >= 128 and N // wn >= 128
         return _choose_instr(M, N, K, dt, small_first=big)

@@ -126,19 +126,23 @@ def test_matmul_uses_mfma(dt, ptr):
         args[n] = (tp.int32, D16)
     for n in ("sak", "sbn", "scn"):
         args[n] = (tp.int32, {"eq1": True})
+    # 8 waves of 64x64: the 32x32x16 MFMA
     src, lds = compile_source(W.matmul_kernel, args,
-                              {"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, num_warps=4,
-                              num_stages=2)
-    assert "newt::mfma_32x32x16" in src
+                              {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 32}, num_warps=8,
+                              num_stages=4)
+    assert "newt::mfma_32x32x16" in src and "newt::mfma_16x16x32" not in src
     assert 0 < lds <= 160 * 1024
     asm = isa(src)
     assert f"v_mfma_f32_32x32x16_{dt}" in asm
     assert "ds_read_b128" in asm
-    # 4 waves of 128x128 over one 32-deep k-step: the 16x16x32 MFMA
-    src, lds = compile_source(W.matmul_kernel, args,
-                              {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, num_warps=4,
-                              num_stages=4)
-    assert "newt::mfma_16x16x32" in src and lds == 128 * 1024
+    # one wave per SIMD (4-wave workgroups): the 16x16x32 MFMA, whatever the
+    # wave tile and k-step
+    for cex, ns in (({"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32}, 4),
+                    ({"BLOCK_M": 128, "BLOCK_N": 128, "BLOCK_K": 64}, 4),
+                    ({"BLOCK_M": 64, "BLOCK_N": 64, "BLOCK_K": 64}, 4)):
+        src, lds = compile_source(W.matmul_kernel, args, cex, num_warps=4, num_stages=ns)
+        assert "newt::mfma_16x16x32" in src and "newt::mfma_32x32x16" not in src, cex
+    assert lds == 64 * 64 * 2 * 2 * 4
     assert f"v_mfma_f32_16x16x32_{dt}" in isa(src)
 
 
