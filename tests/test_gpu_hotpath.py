@@ -254,6 +254,24 @@ def test_attention_default_config(W, causal, B, H, S, D):
     assert orc.rel_frobenius(npf(o), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("BM,BN,warps", [(256, 32, 8), (128, 32, 4), (128, 128, 4), (64, 32, 2)])
+def test_attention_key_block_sizes(W, causal, D, BM, BN, warps):
+    """Key blocks of 32 and 128 (one and four 16x16x32 P @ V steps per block,
+    the score accumulator fed in place) and 16 to 32 query rows per wave, on a
+    ragged sequence, both kernels."""
+    q, k, v = (seeded((1, 2, 333, D), s, dtype=torch.bfloat16) for s in (36, 37, 38))
+    ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
+                        out_dtype="bfloat16")
+    for plain in (False, True):
+        print(f"attention D={D} BM={BM} BN={BN} warps={warps} causal={causal} plain={plain}",
+              flush=True)
+        o = W.attention(q, k, v, causal=causal, plain=plain, BLOCK_M=BM, BLOCK_N=BN,
+                        num_warps=warps)
+        assert orc.rel_frobenius(npf(o), ref) <= 1e-2, plain
+
+
 @pytest.mark.parametrize("B,H,S", [(1, 8, 1000), (2, 8, 300), (3, 8, 777), (1, 24, 513),
                                    (1, 32, 300), (2, 32, 300), (1, 96, 200)])
 def test_attention_causal_heads_split_over_xcds(W, B, H, S):
