@@ -1099,8 +1099,10 @@ class DotPipeline:
         # k-slot e of a lane maps to the column its accumulator register holds
         # (32x32: kk + 8*(e/4) + 4h + e%4 for lane half h; 16x16: kk +
         # 16*(e/4) + 4g + e%4 for lane group g, two accumulator tiles per MFMA)
+        # (an [M, K] accumulator of this instruction exists only when K is a
+        # multiple of its tile width: a 16-wide P never is one of 32x32x16)
         perm = (orient == "row" and isinstance(a, Reg) and isinstance(Bt, Staged)
-                and wn == 1 and a.layout == lo.mfma_c(M, K, instr, wm, 1, "row")
+                and wn == 1 and K % MI == 0 and a.layout == lo.mfma_c(M, K, instr, wm, 1, "row")
                 and (MI == 32 or os.environ.get("NEWT_PERM16", "1") != "0"))
         srcs = []
         for role, X in (("A", a), ("B", Bt)):

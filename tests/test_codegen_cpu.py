@@ -627,6 +627,24 @@ def test_chained_dot_reads_v_in_accumulator_order(monkeypatch, mode, instr, v_ke
     assert "_cv" not in src
 
 
+def test_chained_dot_with_a_16_wide_p_compiles():
+    """16-key blocks: the score tile is 16 wide, so P @ V (K = 16) takes
+    32x32x16 and P goes through an LDS conversion; the in-place check must not
+    build a 32x32 accumulator layout for a 16-wide P (it asserted here)."""
+    args = {"a_ptr": (F16P, A16), "k_ptr": (F16P, A16), "v_ptr": (F16P, A16),
+            "o_ptr": (F32P, A16), "s_ptr": (F32P, A16), "N": (tp.int32, D16),
+            "svn": (tp.int32, D16), "svd": (tp.int32, {"eq1": True})}
+    for BM, D, w in ((128, 64, 4), (64, 32, 2)):
+        src, _ = compile_source(_chained_dots_kernel, args, {"BLOCK_M": BM, "BLOCK_N": 16, "D": D},
+                                num_warps=w, num_stages=2)
+        assert "newt::mfma_32x32x16" in src and "_perm" not in src
+    for kern in (W.attention_kernel, W.attention_plain_kernel):
+        src, _ = compile_source(kern, _attention_args(), {"BLOCK_M": 128, "BLOCK_N": 16, "D": 64,
+                                                          "CAUSAL": True},
+                                num_warps=4, num_stages=2)
+        assert "_perm" not in src
+
+
 def test_attention_program_ids_not_grouped():
     args = {n: (BF16P, A16) for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
     args.update({"S": (tp.int32, D16), "H": (tp.int32, D16), "scale": tp.float32})

@@ -256,11 +256,15 @@ def test_attention_default_config(W, causal, B, H, S, D):
 
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("BM,BN,warps", [(256, 32, 8), (128, 32, 4), (128, 128, 4), (64, 32, 2)])
+@pytest.mark.parametrize("BM,BN,warps", [(256, 32, 8), (128, 32, 4), (128, 128, 4), (64, 32, 2),
+                                         (128, 16, 4)])
 def test_attention_key_block_sizes(W, causal, D, BM, BN, warps):
     """Key blocks of 32 and 128 (one and four 16x16x32 P @ V steps per block,
     the score accumulator fed in place) and 16 to 32 query rows per wave, on a
-    ragged sequence, both kernels."""
+    ragged sequence, both kernels. 16-key blocks fit no 16x16x32 step: P @ V
+    runs on 32x32x16 with P converted through LDS (this configuration failed
+    to compile while the in-place check built a 32-wide accumulator layout
+    for the 16-wide P)."""
     q, k, v = (seeded((1, 2, 333, D), s, dtype=torch.bfloat16) for s in (36, 37, 38))
     ref = orc.attention(npf(q), npf(k), npf(v), D ** -0.5, causal, p_dtype="bfloat16",
                         out_dtype="bfloat16")
