@@ -234,6 +234,7 @@ def bracketed_launches(fn, steps, lead=True):
 
 
 SETTLE_S = 0.4
+MM_WINDOWS = 5   # timed windows per sized-matmul secondary line (median reported)
 
 
 def settle_clocks(fn, seconds):
@@ -941,8 +942,11 @@ def secondary(cpu=True, cpu_budget=2.0):
             warm_up(run)
             # like the headline: K launches queued behind a GPU spin, one event
             # pair around them (at 1024^3 the host's ~30 us per launch would
-            # otherwise leave the GPU idle, and clocking down, between kernels)
-            kern = bracketed_launches(run, 20) / 20
+            # otherwise leave the GPU idle, and clocking down, between kernels).
+            # The median of five such windows: one window of a short kernel
+            # (~0.4 ms at 2048^3) samples a single point of the clock the power
+            # limit moves up and down
+            kern = statistics.median(bracketed_launches(run, 20) / 20 for _ in range(MM_WINDOWS))
             _, kern_ev = timed_launches(run, 20)
             v = 2.0 * S ** 3 / (kern * 1e-3) / 1e12
             dname = {torch.float16: "float16", torch.bfloat16: "bfloat16",
@@ -959,7 +963,8 @@ def secondary(cpu=True, cpu_budget=2.0):
             if dt != torch.float32:
                 for _ in range(3):
                     torch.mm(a, b, out=c)
-                tk = bracketed_launches(lambda: torch.mm(a, b, out=c), 20) / 20
+                tk = statistics.median(bracketed_launches(lambda: torch.mm(a, b, out=c), 20) / 20
+                                       for _ in range(MM_WINDOWS))
                 line["torch_mm_tflops"] = round(2.0 * S ** 3 / (tk * 1e-3) / 1e12, 2)
             if cpu:
                 line["cpu_baseline"] = cpu_matmul(S, dt, cpu_budget,
