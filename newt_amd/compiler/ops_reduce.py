@@ -21,7 +21,7 @@ import math
 import os
 
 from . import types as tp
-from .values import Block, Const, LazyLoad, Reg, Scalar
+from .values import Const, LazyLoad, Reg, Scalar
 
 _OPS = {"sum": "newt::Sum", "max": "newt::Max", "min": "newt::Min"}
 
