@@ -25,7 +25,7 @@ import inspect
 import os
 import textwrap
 
-from ..compiler import CompileError, Param, compile_fn
+from ..compiler import Param, compile_fn
 from ..compiler import types as tp
 from ..compiler.codegen import _CKEYWORDS
 from . import hip as _hip

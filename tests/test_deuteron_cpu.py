@@ -128,7 +128,6 @@ def test_whole_dims_meeting_share_one_span():
 
 
 def test_span_sizes_must_agree():
-    from newt_amd.deuteron.runtime import _Specialization
     x, w = torch.empty(10, 30), torch.empty(31)
     spec = layernorm._specialize((x, w, w, x, 1e-5))
     with pytest.raises(ValueError, match="meet in one expression"):

@@ -169,7 +169,6 @@ def test_launch_fast_path_tracks_specialization(monkeypatch):
     """The launch fast path is keyed on everything the slow path specializes
     on: a call differing in an int's ==1 / divisibility, a constexpr value, a
     launch option or a codegen switch must not reuse another call's kernel."""
-    import newt_amd.runtime.jit as J
 
     @newt.jit
     def k(x_ptr, n, BLOCK: nl.constexpr):
