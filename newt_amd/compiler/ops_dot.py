@@ -103,7 +103,8 @@ class DotOps:
           windows: the 4-wave 256x256x32 matmul tile +3.5%; 2048^3 on the
           128x128x64 4-stage tile +1.2% fp16 and +5-7.5% bf16, other 4-wave
           2048^3 tiles +0.6-1.2%; 1024^3 on 64x64x64 +4-5% with 4 stages, -3%
-          with 3 (the autotuner chooses between them);
+          with 3 (the autotuner chooses between them). Not for 128x128 wave
+          tiles over k-steps deeper than 32, whose 16x16x32 fragments spill;
         - for a column-oriented dot of more waves whose waves each hold a tile
           of at least 128x128 over a single 32-deep k-step (8-wave tiles
           below that ran 2.5-27% slower on 16x16x32: 256x128x32, 256x256x32,
@@ -120,12 +121,16 @@ class DotOps:
         if self.prefer_rows or instr != "32x32x16":
             small = mode == "16" or (self.prefer_rows and self.chained_dots and mode != "32")
             return _choose_instr(M, N, K, dt, small_first=small)
-        if mode or self.W <= 4:
-            return _choose_instr(M, N, K, dt, small_first=mode != "32")
-        if K != 32:
-            return instr
+        if mode:
+            return _choose_instr(M, N, K, dt, small_first=mode == "16")
         wm, wn, _ = self.wave_grid(M, N, instr)
         big = M // wm >= 128 and N // wn >= 128
+        if self.W <= 4:
+            # except 128x128 wave tiles over a deeper k-step: their 16x16x32
+            # fragments spill (256x256x64 on 4 waves: 292 bytes of scratch)
+            return instr if big and K > 32 else _choose_instr(M, N, K, dt, small_first=True)
+        if K != 32:
+            return instr
         return _choose_instr(M, N, K, dt, small_first=big)
 
     def dot_orient(self):

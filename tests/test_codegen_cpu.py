@@ -144,6 +144,11 @@ def test_matmul_uses_mfma(dt, ptr):
         assert "newt::mfma_16x16x32" in src and "newt::mfma_32x32x16" not in src, cex
     assert lds == 64 * 64 * 2 * 2 * 4
     assert f"v_mfma_f32_16x16x32_{dt}" in isa(src)
+    # except 128x128 wave tiles over a 64-deep k-step (their 16x16x32
+    # fragments spill): 32x32x16
+    src, _ = compile_source(W.matmul_kernel, args, {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 64},
+                            num_warps=4, num_stages=2)
+    assert "newt::mfma_32x32x16" in src and "newt::mfma_16x16x32" not in src
 
 
 def test_attention_compiles_with_mfma():
